@@ -1,0 +1,320 @@
+"""Benchmark of the decode hot path on one MI355X.
+
+Headline (BASELINE.json metric, configuration C2 at B=32): one decode step =
+store_kvcache of one new K/V row per sequence + paged decode attention at
+Qwen3-4B geometry (32q / 8kv / 128, bf16, 256-token pages, contexts
+U[512, 4096], 2048-page pool). ``value`` is the step's algorithmic HBM bytes
+divided by its time (GB/s). Inputs are resident in HBM; each timed step is a
+HIP-graph replay, and consecutive steps use disjoint page sets of the pool so
+repeated reads cannot be served by the 256 MB MALL.
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel (split-KV attention main kernel): its
+                algorithmic bytes per launch / its average duration, measured
+                with HIP events around each launch on the launching stream
+  cpu_baseline  the numpy oracle (fp32) on host cores over a bounded sample
+  extra         C3 verify, C4 W8A16 (all shapes x M, cold weights) and the
+                attention op split into main + combine
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --profile-pass   (few launches of each kernel + a copy of
+                                         known size, for rocprofv3 counter runs)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "paged decode/verify attn + W8A16 GEMV: achieved HBM GB/s, % of MI355X peak"
+PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile-pass", action="store_true")
+    return ap.parse_args()
+
+
+# --------------------------------------------------------------------------- helpers
+def graph_of(fn, torch):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def time_replays(graphs, steps, warmup, torch, per_launch=False):
+    """Average ms per replay over ``steps`` replays (cycling through ``graphs``).
+    per_launch: HIP events around every replay (kernel-duration view)."""
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    if per_launch:
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        for i in range(steps):
+            ev[i][0].record()
+            graphs[i % len(graphs)].replay()
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in ev) / steps
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def decode_bytes(lens, hq, hkv, d, eb, store_rows):
+    """Algorithmic bytes of one decode step: every visible K and V row once,
+    q read + o written, the new K/V rows read and written, tables/lengths/slots."""
+    kv = sum(int(L) for L in lens) * hkv * d * eb * 2
+    qo = 2 * len(lens) * hq * d * eb
+    store = store_rows * hkv * d * eb * 2 * 2
+    idx = sum(math.ceil(int(L) / 256) for L in lens) * 4 + 4 * len(lens) * 2
+    return kv + qo + store + idx
+
+
+def attn_bytes(lens, hq, hkv, d, eb, q_rows=1):
+    return sum(int(L) for L in lens) * hkv * d * eb * 2 + 2 * len(lens) * q_rows * hq * d * eb
+
+
+def load_traffic(kernel_key):
+    """Measured HBM bytes per launch from the committed rocprofv3 counter runs
+    (profiles/traffic.json, written from FETCH_SIZE / WRITE_SIZE passes)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t.get(kernel_key, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+# ------------------------------------------------------------------------ CPU baseline
+def cpu_baseline(case, seconds, torch):
+    """numpy oracle (float32) over whole sequences of the C2 case until
+    ``seconds`` of CPU time are spent; GB/s on the same algorithmic bytes."""
+    import numpy as np
+    from oracle import paged_attention as opa
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        threads = 1
+    bt = case["tables"][0]
+    lens = case["lens"].tolist()
+    hq, hkv, d = case["num_q_heads"], case["num_kv_heads"], case["head_dim"]
+    q = case["q"].float().cpu().numpy()
+    done_bytes, spent, seqs = 0, 0.0, 0
+    b = 0
+    while spent < seconds and seqs < 4 * len(lens):
+        L = lens[b]
+        pages = bt[b, :math.ceil(L / 256)].long().to(case["k_cache"].device)
+        kc = case["k_cache"][pages].float().cpu().numpy()
+        vc = case["v_cache"][pages].float().cpu().numpy()
+        table = np.arange(len(pages)).reshape(1, -1)
+        t0 = time.perf_counter()
+        opa.paged_attention(q[b:b + 1], kc, vc, table, [L], case["scale"], dtype=np.float32)
+        spent += time.perf_counter() - t0
+        done_bytes += attn_bytes([L], hq, hkv, d, 2)
+        seqs += 1
+        b = (b + 1) % len(lens)
+    return {"value": round(done_bytes / spent / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"numpy fp32 oracle, {seqs} whole sequences of C2 B={len(lens)} "
+                      f"({spent:.1f} s, {threads} BLAS threads, os.cpu_count()={os.cpu_count()})"}
+
+
+# ----------------------------------------------------------------------------- extras
+def bench_verify(ops, workloads, torch, steps):
+    case = workloads.verify_case(seed=0)
+    dev = "cuda"
+    bt, cuq, cuk = case["table"].to(dev), case["cu_q"].to(dev), case["cu_k"].to(dev)
+    slots = case["slots"].to(dev)
+    out = torch.empty_like(case["q"])
+
+    def step():
+        ops.store_kvcache(case["k_new"], case["v_new"], case["k_cache"], case["v_cache"], slots)
+        ops.paged_attention(case["q"], case["k_cache"], case["v_cache"], bt, case["scale"],
+                            cu_seqlens_k=cuk, cu_seqlens_q=cuq, max_seqlen_q=case["k"] + 1,
+                            out=out)
+    ms = time_replays([graph_of(step, torch)], steps, 10, torch)
+    nbytes = (attn_bytes(case["keys"].tolist(), 32, 8, 128, 2, q_rows=case["k"] + 1)
+              + case["slots"].numel() * 8 * 128 * 2 * 2 * 2)
+    flops = sum(4 * 32 * 128 * (case["k"] + 1) * int(L) for L in case["keys"])
+    return {"config": "C3 verify B=8 q_len 7 (store + attention)", "us": round(ms * 1e3, 2),
+            "GBps": round(nbytes / ms / 1e6, 1), "TFLOPs": round(flops / ms / 1e9, 2),
+            "seed": case["seed_used"]}
+
+
+def bench_w8a16(ops, workloads, torch, steps):
+    rows = []
+    for name, N, K in workloads.W8A16_SHAPES:
+        for M in workloads.W8A16_MS:
+            copies = max(2, math.ceil(2 * 256e6 / (N * K)))  # > 2x MALL of distinct weights
+            base = workloads.w8a16_case(M, N, K, seed=N + M)
+            ws = [base["w"]] + [torch.roll(base["w"], i, 0) for i in range(1, copies)]
+            ss = [base["s"]] * copies
+            y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+            graphs = []
+            for i in range(copies):
+                graphs.append(graph_of(
+                    lambda i=i: ops.w8a16_linear(base["x"], ws[i], ss[i], out=y), torch))
+            ms = time_replays(graphs, max(steps, copies), 5, torch, per_launch=True)
+            nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
+            rows.append({"shape": name, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                         "GBps": round(nbytes / ms / 1e6, 1),
+                         "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4)})
+            del ws, graphs
+            torch.cuda.empty_cache()
+    return rows
+
+
+# ---------------------------------------------------------------------------- profile
+def profile_pass(ops, workloads, torch):
+    """A few launches of each kernel plus a 512 MiB device copy (known bytes) so
+    rocprofv3 counter runs can be scaled; prints what ran."""
+    case = workloads.decode_case(32, seed=0, sets=1)
+    bt = case["tables"][0].cuda()
+    lens = case["lens"].cuda()
+    out = torch.empty_like(case["q"])
+    for _ in range(3):
+        ops.paged_attention(case["q"], case["k_cache"], case["v_cache"], bt, case["scale"],
+                            context_lens=lens, out=out)
+    src = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    c = workloads.w8a16_case(1, 151936, 1024, seed=1)
+    for _ in range(3):
+        ops.w8a16_linear(c["x"], c["w"], c["s"])
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_pass": True, "attn_bytes": attn_bytes(case["lens"].tolist(),
+                                                                     32, 8, 128, 2),
+                      "copy_bytes": 2 * src.numel(),
+                      "lm_head_bytes": 151936 * 1024 + 2 * 151936 + 2048 + 2 * 151936}))
+
+
+# ------------------------------------------------------------------------------- main
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures the one-GPU hot path only: every box in this build has a "
+              "single GPU; run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__
+    __graft_entry__.load_package()
+    from specdec_nanovllm_amd import ops, workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    if args.profile_pass:
+        profile_pass(ops, workloads, torch)
+        return
+
+    B = args.batch
+    hq, hkv, d = 32, 8, 128
+    probe = workloads.decode_case(B, seed=0, sets=1, device="cpu", num_blocks=2048,
+                                  num_q_heads=1, num_kv_heads=1, head_dim=8)
+    pages = sum(math.ceil(int(L) / 256) for L in probe["lens"])
+    sets = max(1, min(6, 2048 // pages))
+    del probe
+    case = workloads.decode_case(B, seed=0, sets=sets)
+    lens = case["lens"]
+    lens_d = lens.cuda()
+    tables = [t.cuda() for t in case["tables"]]
+    slots = [s.cuda() for s in case["slots"]]
+    kc, vc, q = case["k_cache"], case["v_cache"], case["q"]
+    out = torch.empty_like(q)
+
+    def step_fn(i):
+        def f():
+            ops.store_kvcache(case["k_new"], case["v_new"], kc, vc, slots[i])
+            ops.paged_attention(q, kc, vc, tables[i], case["scale"], context_lens=lens_d, out=out)
+        return f
+
+    def main_fn(i):
+        return lambda: ops.paged_attention(q, kc, vc, tables[i], case["scale"],
+                                           context_lens=lens_d, out=out, main_only=True)
+
+    def attn_fn(i):
+        return lambda: ops.paged_attention(q, kc, vc, tables[i], case["scale"],
+                                           context_lens=lens_d, out=out)
+
+    step_graphs = [graph_of(step_fn(i), torch) for i in range(sets)]
+    main_graphs = [graph_of(main_fn(i), torch) for i in range(sets)]
+    attn_graphs = [graph_of(attn_fn(i), torch) for i in range(sets)]
+
+    # ---- timed region: exactly `steps` decode steps
+    torch.cuda.synchronize()
+    ms_step = time_replays(step_graphs, args.steps, args.warmup, torch)
+    step_bytes = decode_bytes(lens.tolist(), hq, hkv, d, 2, B)
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+
+    # ---- dominant kernel: attention main kernel, HIP events around each launch
+    ms_main = time_replays(main_graphs, args.steps, args.warmup, torch, per_launch=True)
+    ms_attn = time_replays(attn_graphs, args.steps, args.warmup, torch, per_launch=True)
+    a_bytes = attn_bytes(lens.tolist(), hq, hkv, d, 2)
+    achieved = a_bytes / (ms_main * 1e-3) / 1e9
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/K/V, seeded page permutations)",
+        "config": {"workload": f"C2 decode step B={B}: store_kvcache + paged decode attention, "
+                               "Qwen3-4B attention 32q/8kv/128, ctx U[512,4096], 256-token "
+                               f"pages, 2048-page pool, {sets} disjoint page sets rotated",
+                   "batch": B, "context_lens_sum": int(lens.sum()),
+                   "algorithmic_bytes_per_step": step_bytes,
+                   "frac_of_peak": round(value / PEAK_HBM_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": load_traffic("paged_attn_main_c2_b32"),
+                     "kernel": "paged_attn_main", "algorithmic_bytes": a_bytes,
+                     "avg_us": round(ms_main * 1e3, 2)},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds, torch)
+    if not args.no_extra:
+        del step_graphs, main_graphs, attn_graphs
+        extra = {"attention_op_us": round(ms_attn * 1e3, 2),
+                 "attention_main_us": round(ms_main * 1e3, 2),
+                 "step_us": round(ms_step * 1e3, 2)}
+        del case, kc, vc
+        torch.cuda.empty_cache()
+        extra["verify"] = bench_verify(ops, workloads, torch, args.steps)
+        torch.cuda.empty_cache()
+        extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100))
+        line["extra"] = extra
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,166 @@
+/*
+ * specdec_amd.h — C ABI of the MI355X (gfx950) decode hot path.
+ *
+ * The library `libspecdec_amd.so` exports exactly the functions below. Every
+ * entry point takes plain device pointers, element strides and sizes, and a
+ * `hipStream_t` passed as `void*` (NULL = the legacy default stream). Nothing
+ * here allocates, frees or synchronises: output buffers and workspaces are
+ * owned by the caller, and every launch is enqueued on the given stream, so
+ * calls can be captured into a HIP graph and issued from several streams at
+ * once (each call uses only the workspace it is handed).
+ *
+ * Return value: SD_OK (0) or a nonzero `sd_status`; the message of the last
+ * failure on the calling thread is returned by `sd_last_error()`.
+ *
+ * Dtype codes: SD_BF16, SD_F16 for activations/caches; scales may also be
+ * SD_F32. Strides are in ELEMENTS of the tensor they describe.
+ */
+#ifndef SPECDEC_AMD_H
+#define SPECDEC_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SD_ABI_VERSION 1
+
+typedef enum sd_status {
+  SD_OK = 0,
+  SD_ERR_VALUE = 1,       /* bad argument: the reference raises AssertionError/ValueError */
+  SD_ERR_UNSUPPORTED = 2, /* valid but not implemented shape/dtype: reference TORCH_CHECK */
+  SD_ERR_WORKSPACE = 3,   /* workspace NULL or smaller than the *_workspace_size() query */
+  SD_ERR_HIP = 4          /* a HIP launch reported an error */
+} sd_status;
+
+typedef enum sd_dtype { SD_BF16 = 0, SD_F16 = 1, SD_F32 = 2 } sd_dtype;
+
+/* ABI version compiled into the library (== SD_ABI_VERSION of its header). */
+int sd_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* sd_last_error(void);
+
+/*
+ * KV-cache slot write.
+ * Replaces `store_kvcache` + `store_kvcache_kernel`
+ * (nanovllm/layers/attention.py:10-40): for every token i with
+ * s = slot_mapping[i] != -1, row i of key/value (num_kv_heads x head_dim) is
+ * copied bit-for-bit to cache position (s / block_size, s % block_size).
+ * Slots outside [0, num_blocks*block_size) are skipped like -1 (the reference
+ * leaves them undefined). Works for any 2- or 4-byte element type.
+ *   key/value  : (num_tokens, num_kv_heads, head_dim), head_dim contiguous
+ *   k/v_cache  : (num_blocks, block_size, num_kv_heads, head_dim) by strides
+ */
+int sd_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+                     const void* value, int64_t value_stride_tok, int64_t value_stride_head,
+                     void* k_cache, void* v_cache, int64_t cache_stride_block,
+                     int64_t cache_stride_pos, int64_t cache_stride_head,
+                     const int32_t* slot_mapping, int64_t num_tokens, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                     int32_t elem_bytes, void* stream);
+
+/*
+ * Bytes of fp32 split-KV workspace that sd_paged_attention needs for these
+ * sizes (0 is a valid answer when no split is ever used).
+ *   max_ctx     : block_table width * block_size (static bound, no host sync)
+ *   num_splits  : maximum KV splits per sequence, 0 = library default
+ */
+size_t sd_paged_attention_workspace_size(int32_t num_seqs, int32_t max_qlen,
+                                         int32_t num_q_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int64_t max_ctx,
+                                         int32_t num_splits);
+
+/*
+ * Paged decode / speculative-verify attention (GQA, split-KV).
+ * Replaces the decode call `flash_attn_with_kvcache(q, k_cache, v_cache,
+ * cache_seqlens, block_table, softmax_scale, causal=True)`
+ * (nanovllm/layers/attention.py:71-81), the paged verify call
+ * `flash_attn_varlen_func(..., causal=True, block_table)` (attention.py:64-70
+ * with model_runner.py:492-584), and the standalone kernels
+ * `paged_decode_attention` (nanovllm/kernels/paged_decode_attn.py:352-469) and
+ * `paged_decode_cuda` (nanovllm/kernels/paged_decode_attn_cuda.cu:1388-1453).
+ *
+ * Sequence b has L_b keys (context_lens[b], or cu_seqlens_k[b+1]-cu_seqlens_k[b]
+ * when context_lens is NULL) and n_b query rows starting at token
+ * cu_seqlens_q[b] (or n_b = 1 at token b when cu_seqlens_q is NULL). Query row
+ * i of sequence b attends keys [0, L_b - n_b + i] (bottom-right causal; for
+ * n_b = 1 that is all L_b keys). Key position p is read from page
+ * block_table[b, p / block_size], row p % block_size. A row with no visible
+ * key (L_b = 0 padding rows) produces zeros. Query rows at or beyond total_q
+ * (the first dimension of q and out) are never read or written, and L_b is
+ * clamped into [0, max_blocks_per_seq * block_size].
+ *   q      : (total_q, num_q_heads, head_dim)
+ *   out    : (total_q, num_q_heads, head_dim), same dtype as q
+ *   caches : (num_blocks, block_size, num_kv_heads, head_dim) by strides
+ *            (interleaved or head-major page layouts both work)
+ * Supported: head_dim 128, dtype bf16/f16, (num_q_heads/num_kv_heads) *
+ * max_qlen <= 32. Page ids are clamped into [0, num_blocks).
+ * workspace: >= sd_paged_attention_workspace_size(...) bytes (may be NULL if
+ * that is 0). num_splits: maximum splits per sequence, 0 = library default.
+ */
+int sd_paged_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                       const void* k_cache, const void* v_cache, int64_t cache_stride_block,
+                       int64_t cache_stride_pos, int64_t cache_stride_head, int64_t num_blocks,
+                       int32_t block_size, const int32_t* block_table, int64_t bt_stride,
+                       int32_t max_blocks_per_seq, const int32_t* context_lens,
+                       const int32_t* cu_seqlens_k, const int32_t* cu_seqlens_q,
+                       int32_t max_qlen, int64_t total_q, int32_t num_seqs, int32_t num_q_heads,
+                       int32_t num_kv_heads, int32_t head_dim, float scale, int32_t dtype,
+                       void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                       void* workspace, size_t workspace_bytes, int32_t num_splits,
+                       void* stream);
+
+/*
+ * Same arguments as sd_paged_attention, but only the split-KV main kernel
+ * runs: `out` receives the rows of sequences that fit in one split and the
+ * workspace receives the partial (m, l, acc) of the others. Measurement twin
+ * of `paged_decode_cuda_partial` (nanovllm/kernels/paged_decode_attn_cuda.cu:1558-1593).
+ */
+int sd_paged_attention_partial(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                               const void* k_cache, const void* v_cache,
+                               int64_t cache_stride_block, int64_t cache_stride_pos,
+                               int64_t cache_stride_head, int64_t num_blocks,
+                               int32_t block_size, const int32_t* block_table,
+                               int64_t bt_stride, int32_t max_blocks_per_seq,
+                               const int32_t* context_lens, const int32_t* cu_seqlens_k,
+                               const int32_t* cu_seqlens_q, int32_t max_qlen,
+                               int64_t total_q, int32_t num_seqs, int32_t num_q_heads,
+                               int32_t num_kv_heads,
+                               int32_t head_dim, float scale, int32_t dtype, void* out,
+                               int64_t out_stride_tok, int64_t out_stride_head,
+                               void* workspace, size_t workspace_bytes,
+                               int32_t num_splits, void* stream);
+
+/*
+ * Bytes of fp32 split-K workspace that sd_w8a16_linear needs for this shape.
+ */
+size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_size);
+
+/*
+ * W8A16 weight-only linear: y = x @ (w * scale)^T (+ bias).
+ * Replaces `int8_linear` with `_int8_dequant_gemm_kernel` and
+ * `_splitk_reduce_kernel` (nanovllm/layers/quant.py:165-310).
+ *   x     : (M, K) dtype (bf16/f16), row stride x_stride_m, K contiguous
+ *   w     : (N, K) int8, row stride w_stride_n, K contiguous
+ *   scale : (N,) when group_size == 0 (per channel), else (N, K/group_size)
+ *           row-major; scale_dtype bf16/f16/f32
+ *   bias  : (N,) dtype or NULL
+ *   y     : (M, N) dtype, row stride y_stride_m
+ * Dequantization is fused (int8 -> fp in registers, fp32 accumulation, scale
+ * applied to the fp32 accumulator). Supported: K % 64 == 0, group_size 0 or a
+ * multiple of 64 dividing K.
+ */
+int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t w_stride_n,
+                    const void* scale, int32_t scale_dtype, int32_t group_size,
+                    const void* bias, void* y, int64_t y_stride_m, int64_t M, int64_t N,
+                    int64_t K, int32_t dtype, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPECDEC_AMD_H */

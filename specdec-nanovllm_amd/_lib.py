@@ -1,0 +1,126 @@
+"""ctypes binding of ``libspecdec_amd.so`` — the C ABI declared in
+``include/specdec_amd.h``.
+
+torch is imported before the library is opened: the library needs
+``libamdhip64.so.7`` by soname, and loading it after torch makes it bind to
+the HIP runtime torch already mapped (one runtime per process, so streams and
+device pointers are shared). There is no fallback: if the library is missing
+or was built for another ABI, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libspecdec_amd.so")
+ABI_VERSION = 1
+
+SD_OK, SD_ERR_VALUE, SD_ERR_UNSUPPORTED, SD_ERR_WORKSPACE, SD_ERR_HIP = range(5)
+SD_BF16, SD_F16, SD_F32 = 0, 1, 2
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/specdec_amd.h one to one.
+SIGNATURES = {
+    "sd_abi_version": (ctypes.c_int, []),
+    "sd_last_error": (ctypes.c_char_p, []),
+    "sd_store_kvcache": (ctypes.c_int, [
+        _p, _i64, _i64,            # key, strides (tok, head)
+        _p, _i64, _i64,            # value, strides
+        _p, _p, _i64, _i64, _i64,  # k_cache, v_cache, strides (block, pos, head)
+        _p, _i64,                  # slot_mapping, num_tokens
+        _i32, _i32, _i32, _i64,    # num_kv_heads, head_dim, block_size, num_blocks
+        _i32, _p]),                # elem_bytes, stream
+    "sd_paged_attention_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i64, _i32]),
+    "sd_paged_attention": (ctypes.c_int, [
+        _p, _i64, _i64,                 # q, strides (tok, head)
+        _p, _p, _i64, _i64, _i64, _i64,  # k_cache, v_cache, strides, num_blocks
+        _i32, _p, _i64, _i32,           # block_size, block_table, bt_stride, max_blocks
+        _p, _p, _p,                     # context_lens, cu_seqlens_k, cu_seqlens_q
+        _i32, _i64, _i32, _i32, _i32, _i32,  # max_qlen, total_q, seqs, hq, hkv, head_dim
+        _f32, _i32,                     # scale, dtype
+        _p, _i64, _i64,                 # out, strides
+        _p, _sz, _i32, _p]),            # workspace, bytes, num_splits, stream
+    "sd_w8a16_workspace_size": (_sz, [_i64, _i64, _i64, _i32]),
+    "sd_w8a16_linear": (ctypes.c_int, [
+        _p, _i64, _p, _i64,             # x, x_stride, w, w_stride
+        _p, _i32, _i32, _p,             # scale, scale_dtype, group_size, bias
+        _p, _i64,                       # y, y_stride
+        _i64, _i64, _i64, _i32,         # M, N, K, dtype
+        _p, _sz, _p]),                  # workspace, bytes, stream
+}
+SIGNATURES["sd_paged_attention_partial"] = SIGNATURES["sd_paged_attention"]
+
+_lib = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Open the library (once) and declare every exported signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+            "g.build()'` (hipcc, gfx950). There is no CPU fallback.")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    ver = lib.sd_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"libspecdec_amd ABI {ver} != expected {ABI_VERSION}; rebuild")
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    """Map a nonzero sd_status to the exception the reference raises."""
+    if rc == SD_OK:
+        return
+    msg = load().sd_last_error().decode(errors="replace")
+    if rc == SD_ERR_VALUE:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+_DTYPES = {torch.bfloat16: SD_BF16, torch.float16: SD_F16, torch.float32: SD_F32}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPES[dt]
+    except KeyError:
+        raise RuntimeError(f"unsupported dtype {dt}") from None
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors on one ROCm device; returns it. CPU tensors are an error (no fallback)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"specdec_nanovllm_amd ops run only on a ROCm GPU; got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def stream_ptr(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream

@@ -1,0 +1,93 @@
+// sd_common.h — shared device/host helpers for the gfx950 kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * wave64: `lane` = threadIdx.x & 63, `wave` = threadIdx.x >> 6;
+//  * 16-byte global loads/stores (`u32x4`), LDS rows padded so that the
+//    column reads of the MFMA operand gathers are bank-conflict free;
+//  * MFMA v_mfma_f32_16x16x32_{bf16,f16} operand layout (CDNA4):
+//      A (16 x 32):  lane l holds A[l % 16][8 * (l / 16) + j], j = 0..7
+//      B (32 x 16):  lane l holds B[8 * (l / 16) + j][l % 16], j = 0..7
+//      D (16 x 16):  lane l holds D[4 * (l / 16) + i][l % 16], i = 0..3
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "specdec_amd.h"
+
+namespace sd {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- dtypes
+// Element traits: `T` is the 16-bit storage type (__bf16 or _Float16).
+template <typename T> struct Elem;
+template <> struct Elem<__bf16> {
+  typedef bf16x8 vec8;
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Elem<_Float16> {
+  typedef f16x8 vec8;
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// fp32 -> 16-bit storage bits, round to nearest even.
+template <typename T> __device__ __forceinline__ uint16_t to_bits(float x) {
+  return __builtin_bit_cast(uint16_t, static_cast<T>(x));
+}
+// Pack two fp32 into one dword of two 16-bit values (lo in bits 0..15).
+template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return static_cast<uint32_t>(to_bits<T>(lo)) | (static_cast<uint32_t>(to_bits<T>(hi)) << 16);
+}
+template <typename T> __device__ __forceinline__ float from_bits(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(T, b));
+}
+// Split two fp32 values into 16-bit hi parts and 16-bit parts of the remainder:
+// a = float(hi_a) + float(lo_a) to ~2^-17 relative (hi and lo each RNE).
+template <typename T>
+__device__ __forceinline__ void split_pack(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const T ha = static_cast<T>(a), hb = static_cast<T>(b);
+  hi = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
+       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
+  lo = pack2<T>(a - static_cast<float>(ha), b - static_cast<float>(hb));
+}
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void store16(void* p, u32x4 v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+// Butterfly max/sum over the four lane groups that share `l % 16`.
+__device__ __forceinline__ float max_over_groups(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float sum_over_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// --------------------------------------------------------------- host side
+// Thread-local message of the last failure (returned by sd_last_error()).
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+// Maps a pending HIP launch error into SD_ERR_HIP with `what` in the message.
+int check_launch(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace sd

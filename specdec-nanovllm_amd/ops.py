@@ -1,0 +1,192 @@
+"""Torch-facing wrappers of the three hot-path kernels.
+
+Each function validates shapes the way the reference does (``assert`` where the
+reference asserts), allocates the output and the split workspace with torch's
+caching allocator on the current stream (so the call is graph-capturable and
+reentrant across streams), and enqueues the HIP kernels through the C ABI on
+``torch.cuda.current_stream()``. Nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _workspace(nbytes: int, dev: torch.device) -> torch.Tensor | None:
+    if nbytes <= 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _i32(t: torch.Tensor | None) -> torch.Tensor | None:
+    if t is None:
+        return None
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return t.contiguous()
+
+
+# --------------------------------------------------------------------------- store
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Write token rows of key/value into the paged cache at ``slot_mapping``.
+
+    Contract of ``store_kvcache`` (nanovllm/layers/attention.py:33-40): key and
+    value are (N, num_kv_heads, head_dim) with contiguous heads, the caches are
+    (num_blocks, block_size, num_kv_heads, head_dim) with stride(1) equal to
+    num_kv_heads * head_dim, and slot -1 skips the row.
+    """
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    assert slot_mapping.numel() == N
+    assert k_cache.stride() == v_cache.stride() and k_cache.shape == v_cache.shape
+    assert key.dtype == value.dtype == k_cache.dtype == v_cache.dtype
+    assert k_cache.dim() == 4 and k_cache.shape[2] == num_heads and k_cache.shape[3] == head_dim
+    dev = _lib.require_device(key, value, k_cache, v_cache, slot_mapping)
+    if N == 0:
+        return
+    slots = _i32(slot_mapping.reshape(-1))
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.sd_store_kvcache(
+            key.data_ptr(), key.stride(0), key.stride(1),
+            value.data_ptr(), value.stride(0), value.stride(1),
+            k_cache.data_ptr(), v_cache.data_ptr(),
+            k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+            slots.data_ptr(), N, num_heads, head_dim, k_cache.shape[1], k_cache.shape[0],
+            key.element_size(), _lib.stream_ptr(dev))
+    _lib.check(rc)
+
+
+# ----------------------------------------------------------------------- attention
+def _cache_geometry(k_cache: torch.Tensor, layout: str):
+    if layout == "head_major":
+        # (num_blocks, num_kv_heads, block_size, head_dim)
+        num_blocks, num_kv_heads, block_size, head_dim = k_cache.shape
+        sb, sh, sp = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    elif layout == "interleaved":
+        # (num_blocks, block_size, num_kv_heads, head_dim): nano-vllm / flash-attn layout
+        num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
+        sb, sp, sh = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    else:
+        raise ValueError(f"unknown layout: {layout}")
+    return num_blocks, block_size, num_kv_heads, head_dim, sb, sp, sh
+
+
+def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    block_table: torch.Tensor, scale: float, *,
+                    context_lens: torch.Tensor | None = None,
+                    cu_seqlens_k: torch.Tensor | None = None,
+                    cu_seqlens_q: torch.Tensor | None = None, max_seqlen_q: int = 1,
+                    layout: str = "interleaved", num_splits: int = 0,
+                    out: torch.Tensor | None = None, main_only: bool = False) -> torch.Tensor:
+    """Paged decode (``cu_seqlens_q is None``: one query row per sequence) or
+    speculative-verify attention (rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]``,
+    bottom-right causal), GQA, split-KV.
+
+    q: (total_q, num_q_heads, head_dim); keys per sequence from ``context_lens``
+    (B,) or ``cu_seqlens_k`` (B+1,). Returns ``out`` (same shape/dtype as q).
+    ``main_only`` runs only the split-KV main kernel (measurement twin).
+    """
+    if q.dim() != 3:
+        raise ValueError(f"q must be (tokens, heads, head_dim), got {tuple(q.shape)}")
+    total_q, num_q_heads, head_dim = q.shape
+    num_blocks, block_size, num_kv_heads, hd_c, sb, sp, sh = _cache_geometry(k_cache, layout)
+    assert num_q_heads % num_kv_heads == 0, \
+        f"GQA needs num_q_heads divisible by num_kv_heads: {num_q_heads} vs {num_kv_heads}"
+    assert hd_c == head_dim, f"head_dim mismatch: q {head_dim} vs cache {hd_c}"
+    assert k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride()
+    assert k_cache.dtype == v_cache.dtype == q.dtype, "q and caches must share one dtype"
+    assert k_cache.stride(-1) == 1 and q.stride(-1) == 1
+    assert block_table.dim() == 2, "block_table must be (num_seqs, max_blocks)"
+    if (context_lens is None) == (cu_seqlens_k is None):
+        raise ValueError("give exactly one of context_lens / cu_seqlens_k")
+    dev = _lib.require_device(q, k_cache, v_cache, block_table, context_lens, cu_seqlens_k,
+                              cu_seqlens_q, out)
+    num_seqs = block_table.shape[0]
+    bt = _i32(block_table)
+    ctx = _i32(context_lens)
+    cuk = _i32(cu_seqlens_k)
+    cuq = _i32(cu_seqlens_q)
+    if cuq is None:
+        max_seqlen_q = 1
+        if total_q != num_seqs:
+            raise ValueError(f"decode expects one query row per sequence: q has {total_q} rows, "
+                             f"block_table {num_seqs}")
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        assert out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
+    if num_seqs == 0 or total_q == 0:
+        return out
+    lib = _lib.load()
+    max_blocks = bt.shape[1]
+    ws_bytes = lib.sd_paged_attention_workspace_size(
+        num_seqs, int(max_seqlen_q), num_q_heads, num_kv_heads, head_dim,
+        max_blocks * block_size, int(num_splits))
+    ws = _workspace(ws_bytes, dev)
+    fn = lib.sd_paged_attention_partial if main_only else lib.sd_paged_attention
+    with torch.cuda.device(dev):
+        rc = fn(q.data_ptr(), q.stride(0), q.stride(1),
+                k_cache.data_ptr(), v_cache.data_ptr(), sb, sp, sh, num_blocks,
+                block_size, bt.data_ptr(), bt.stride(0), max_blocks,
+                _ptr(ctx), _ptr(cuk), _ptr(cuq),
+                int(max_seqlen_q), total_q, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                float(scale), _lib.dtype_code(q.dtype),
+                out.data_ptr(), out.stride(0), out.stride(1),
+                _ptr(ws), ws_bytes, int(num_splits), _lib.stream_ptr(dev))
+    _lib.check(rc)
+    return out
+
+
+# -------------------------------------------------------------------------- w8a16
+def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
+                 bias: torch.Tensor | None = None, group_size: int = 0,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ (qweight * scale)^T + bias with the dequantization fused.
+
+    x: (..., K) fp16/bf16; qweight: (N, K) int8; scale: (N,) when
+    ``group_size == 0`` else (N, K // group_size); returns (..., N) in x.dtype.
+    """
+    assert qweight.dtype == torch.int8, f"qweight must be int8, got {qweight.dtype}"
+    assert qweight.dim() == 2
+    N, K = qweight.shape
+    x2 = x.reshape(-1, x.shape[-1])
+    M = x2.shape[0]
+    assert x2.shape[1] == K, f"K mismatch: x {tuple(x2.shape)} vs w {tuple(qweight.shape)}"
+    if x2.stride(-1) != 1 or (M > 1 and x2.stride(0) % 8 != 0):
+        x2 = x2.contiguous()
+    qw = qweight if qweight.is_contiguous() else qweight.contiguous()
+    sc = scale.contiguous()
+    if group_size:
+        assert sc.numel() == N * (K // group_size), "per-group scale must be (N, K // group_size)"
+    else:
+        assert sc.numel() == N, "per-channel scale must have N entries"
+    b = None if bias is None else bias.to(x.dtype).contiguous()
+    dev = _lib.require_device(x2, qw, sc, b, out)
+    if out is None:
+        y = torch.empty((M, N), device=dev, dtype=x.dtype)
+    else:
+        y = out.reshape(M, N)
+        assert y.dtype == x.dtype and y.stride(-1) == 1
+    if M == 0:
+        return y.view(*x.shape[:-1], N)
+    lib = _lib.load()
+    ws_bytes = lib.sd_w8a16_workspace_size(M, N, K, int(group_size))
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.sd_w8a16_linear(
+            x2.data_ptr(), x2.stride(0), qw.data_ptr(), qw.stride(0),
+            sc.data_ptr(), _lib.dtype_code(sc.dtype), int(group_size), _ptr(b),
+            y.data_ptr(), y.stride(0), M, N, K, _lib.dtype_code(x.dtype),
+            _ptr(ws), ws_bytes, _lib.stream_ptr(dev))
+    _lib.check(rc)
+    return y.view(*x.shape[:-1], N)

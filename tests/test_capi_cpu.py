@@ -1,0 +1,119 @@
+"""The C-ABI library without a GPU: it opens, exports exactly what
+include/specdec_amd.h declares, the ctypes table matches the header's
+parameter counts, and argument validation (which returns before any HIP call)
+reports the reference's error kinds. No kernel is launched here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from specdec_nanovllm_amd import _lib, ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "specdec_amd.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(sd_[a-z_0-9]+)\s*\(([^;]*?)\)\s*;",
+                         text, flags=re.M | re.S):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_header_parses():
+    fns = header_functions()
+    assert {"sd_abi_version", "sd_last_error", "sd_store_kvcache", "sd_paged_attention",
+            "sd_paged_attention_partial", "sd_paged_attention_workspace_size",
+            "sd_w8a16_linear", "sd_w8a16_workspace_size"} <= set(fns)
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.library_path()],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    fns = header_functions()
+    assert set(fns) <= exported, f"missing: {set(fns) - exported}"
+    assert {s for s in exported if s.startswith("sd_")} == set(fns), "undeclared sd_ exports"
+    for name in fns:
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
+
+
+def test_ctypes_table_matches_header_arity():
+    fns = header_functions()
+    assert set(_lib.SIGNATURES) == set(fns)
+    for name, n in fns.items():
+        assert len(_lib.SIGNATURES[name][1]) == n, name
+
+
+def test_abi_version_and_empty_error():
+    lib = _lib.load()
+    assert lib.sd_abi_version() == _lib.ABI_VERSION == 1
+    assert isinstance(lib.sd_last_error(), bytes)
+
+
+def test_validation_errors_without_gpu():
+    lib = _lib.load()
+    # GQA divisibility -> SD_ERR_VALUE (reference: AssertionError / ValueError kind)
+    rc = lib.sd_paged_attention(1, 0, 0, 1, 1, 0, 0, 0, 1, 256, 1, 1, 1, 1, None, None, 1, 1, 1,
+                                30, 8, 128, 0.1, 0, 1, 0, 0, None, 0, 0, None)
+    assert rc == _lib.SD_ERR_VALUE and b"GQA" in lib.sd_last_error()
+    with pytest.raises(ValueError):
+        _lib.check(rc)
+    # head_dim 64 -> SD_ERR_UNSUPPORTED (reference: TORCH_CHECK -> RuntimeError)
+    rc = lib.sd_paged_attention(16, 0, 0, 16, 16, 0, 0, 0, 1, 256, 16, 1, 1, 16, None, None, 1,
+                                1, 1, 32, 8, 64, 0.1, 0, 16, 0, 0, None, 0, 0, None)
+    assert rc == _lib.SD_ERR_UNSUPPORTED
+    with pytest.raises(RuntimeError):
+        _lib.check(rc)
+    # G * q_len > 32 unsupported
+    rc = lib.sd_paged_attention(16, 0, 0, 16, 16, 0, 0, 0, 1, 256, 16, 1, 1, 16, None, 16, 9,
+                                9, 1, 32, 8, 128, 0.1, 0, 16, 0, 0, None, 0, 0, None)
+    assert rc == _lib.SD_ERR_UNSUPPORTED
+    # split workspace missing -> SD_ERR_WORKSPACE
+    rc = lib.sd_paged_attention(16, 4096, 128, 16, 16, 256 * 1024, 1024, 128, 64, 256, 16, 16,
+                                16, 16, None, None, 1, 32, 32, 32, 8, 128, 0.1, 0, 16, 4096,
+                                128, None, 0, 0, None)
+    assert rc == _lib.SD_ERR_WORKSPACE
+    # W8A16: K % 64 != 0 unsupported, M < 0 invalid
+    assert lib.sd_w8a16_linear(16, 96, 16, 96, 16, 1, 0, None, 16, 64, 1, 64, 96, 1, None, 0,
+                               None) == _lib.SD_ERR_UNSUPPORTED
+    assert lib.sd_w8a16_linear(16, 96, 16, 96, 16, 1, 0, None, 16, 64, -1, 64, 96, 1, None, 0,
+                               None) == _lib.SD_ERR_VALUE
+    # store: bad element size
+    assert lib.sd_store_kvcache(16, 0, 0, 16, 0, 0, 16, 16, 0, 0, 0, 16, 1, 1, 8, 16, 1, 3,
+                                None) == _lib.SD_ERR_UNSUPPORTED
+
+
+def test_workspace_queries():
+    lib = _lib.load()
+    # C2 B=32: 16 splits of 256 tokens, 4 rows, (m, l) + 128 fp32 per row
+    n = lib.sd_paged_attention_workspace_size(32, 1, 32, 8, 128, 4096, 0)
+    entries = 32 * 8 * 16 * 4
+    assert n == (entries * 8 + 255) // 256 * 256 + entries * 128 * 4
+    assert lib.sd_paged_attention_workspace_size(1, 1, 32, 8, 128, 128, 0) == 0  # one split
+    assert lib.sd_w8a16_workspace_size(1, 151936, 1024, 0) == 0  # lm_head: no split-K
+    assert lib.sd_w8a16_workspace_size(1, 1024, 3072, 0) > 0      # down: split-K partials
+
+
+def test_ops_refuse_cpu_tensors():
+    # the product path never falls back to CPU math
+    k = torch.zeros((2, 16, 2, 128), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.store_kvcache(torch.zeros((1, 2, 128), dtype=torch.bfloat16),
+                          torch.zeros((1, 2, 128), dtype=torch.bfloat16), k, k.clone(),
+                          torch.zeros(1, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.paged_attention(torch.zeros((1, 4, 128), dtype=torch.bfloat16), k, k,
+                            torch.zeros((1, 1), dtype=torch.int32), 0.1,
+                            context_lens=torch.ones(1, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.w8a16_linear(torch.zeros((1, 64), dtype=torch.float16),
+                         torch.zeros((8, 64), dtype=torch.int8), torch.ones(8))

@@ -1,0 +1,320 @@
+"""GPU parity of paged decode / verify attention against the numpy oracle.
+
+Tolerance: |o - ref| <= 2e-3 + 1e-2 |ref| elementwise,
+ref = float64 attention of the same bf16/fp16 inputs. Covers the C1/C2/C3
+configurations, edge lengths around the 32/64/256-token tiles and pages,
+padding rows, split counts, page sizes, head-major pages, GQA ratios, fp16,
+ragged verify rows, placement/width invariance, determinism and HIP-graph
+replay, plus the reference-mirror entry points and their error behaviour.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_attn, to_np
+from oracle import kvcache as okv
+from oracle import paged_attention as opa
+from specdec_nanovllm_amd import ops, workloads
+from specdec_nanovllm_amd.flash_attn_compat import flash_attn_varlen_func, flash_attn_with_kvcache
+from specdec_nanovllm_amd.kernels.paged_decode_attn import paged_decode_attention
+from specdec_nanovllm_amd.kernels.paged_decode_attn_cuda import paged_decode_attention_cuda
+from specdec_nanovllm_amd.layers.attention import Attention
+from specdec_nanovllm_amd.utils.context import reset_context, set_context
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def compact(k_cache, v_cache, bt):
+    """Copy only the pages a table uses to the host (as float32) and remap the
+    table onto them, so the oracle never touches the whole pool."""
+    bt = bt.cpu()
+    used = sorted(set(int(x) for x in bt.flatten().tolist() if x >= 0))
+    remap = {p: i for i, p in enumerate(used)}
+    idx = torch.tensor(used if used else [0], dtype=torch.long, device=k_cache.device)
+    kc = to_np(k_cache[idx]).astype(np.float32)
+    vc = to_np(v_cache[idx]).astype(np.float32)
+    bt2 = np.array([[remap.get(int(x), -1) for x in row] for row in bt.tolist()],
+                   dtype=np.int64).reshape(bt.shape)
+    return kc, vc, bt2
+
+
+def oracle(q, k_cache, v_cache, bt, lens, scale, cu_q=None):
+    kc, vc, bt2 = compact(k_cache, v_cache, bt)
+    cu = None if cu_q is None else cu_q.cpu().numpy()
+    return opa.paged_attention(to_np(q), kc, vc, bt2, lens.cpu().numpy(), scale, cu)
+
+
+def random_case(lens, *, hq=32, hkv=8, d=128, bs=256, width=None, dtype=torch.bfloat16,
+                seed=0, spare=3):
+    lens = torch.tensor(lens, dtype=torch.int32)
+    need = sum(max(math.ceil(int(L) / bs), 0) for L in lens)
+    nblk = need + spare
+    g = torch.Generator().manual_seed(seed)
+    w = width or max(max(math.ceil(int(L) / bs) for L in lens), 1)
+    bt = workloads.block_tables_for(lens.tolist(), bs, nblk, g, w)[0]
+    dg = workloads.device_generator(DEV, seed + 1)
+    kc = torch.randn((nblk, bs, hkv, d), generator=dg, device=DEV).to(dtype)
+    vc = torch.randn((nblk, bs, hkv, d), generator=dg, device=DEV).to(dtype)
+    q = torch.randn((len(lens), hq, d), generator=dg, device=DEV).to(dtype)
+    return q, kc, vc, bt, lens
+
+
+def run_decode(q, kc, vc, bt, lens, **kw):
+    return ops.paged_attention(q, kc, vc, bt.to(DEV), q.shape[-1] ** -0.5,
+                               context_lens=lens.to(DEV), **kw)
+
+
+# ------------------------------------------------------------------ BASELINE configs
+@pytest.mark.parametrize("batch", [1, 8, 32])
+def test_c2_decode_step(batch):
+    case = workloads.decode_case(batch, seed=100 + batch)
+    bt, lens, slots = case["tables"][0], case["lens"], case["slots"][0]
+    kc, vc = case["k_cache"], case["v_cache"]
+    ops.store_kvcache(case["k_new"], case["v_new"], kc, vc, slots.to(DEV))
+    out = run_decode(case["q"], kc, vc, bt, lens)
+    torch.cuda.synchronize()
+    # the new rows are in the cache (read back through the table) ...
+    for b in range(batch):
+        p = int(lens[b]) - 1
+        page = int(bt[b, p // 256])
+        assert torch.equal(kc[page, p % 256], case["k_new"][b])
+        assert torch.equal(vc[page, p % 256], case["v_new"][b])
+    # ... and attention over them matches the oracle
+    ref = oracle(case["q"], kc, vc, bt, lens, case["scale"])
+    assert_close_attn(to_np(out), ref, what=f"C2 B={batch}")
+
+
+def test_c1_geometry_bf16():
+    # Qwen3-0.6B attention: 16q/8kv/128, B=1, L=1000, 64-block pool, 4 permuted pages
+    rng = np.random.default_rng(0)
+    bt = torch.from_numpy(rng.permutation(64)[:4].astype(np.int32)).view(1, 4)
+    dg = workloads.device_generator(DEV, 1)
+    kc = torch.randn((64, 256, 8, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    vc = torch.randn((64, 256, 8, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    q = torch.randn((1, 16, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    lens = torch.tensor([1000], dtype=torch.int32)
+    out = run_decode(q, kc, vc, bt, lens)
+    assert_close_attn(to_np(out), oracle(q, kc, vc, bt, lens, 128 ** -0.5), what="C1")
+
+
+def test_c3_verify():
+    case = workloads.verify_case(seed=5)
+    assert case["crosses_page"], "C3 must include rows that straddle a 256-token page"
+    kc, vc = case["k_cache"], case["v_cache"]
+    ops.store_kvcache(case["k_new"], case["v_new"], kc, vc, case["slots"].to(DEV))
+    out = ops.paged_attention(case["q"], kc, vc, case["table"].to(DEV), case["scale"],
+                              cu_seqlens_k=case["cu_k"].to(DEV),
+                              cu_seqlens_q=case["cu_q"].to(DEV), max_seqlen_q=case["k"] + 1)
+    torch.cuda.synchronize()
+    ref = oracle(case["q"], kc, vc, case["table"], case["keys"], case["scale"], case["cu_q"])
+    assert_close_attn(to_np(out), ref, what="C3 verify")
+
+
+# -------------------------------------------------------------------- edge cases
+@pytest.mark.parametrize("L", [1, 2, 7, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257,
+                               300, 511, 512, 513, 1000, 1024, 2049, 4095, 4096])
+def test_edge_lengths(L):
+    q, kc, vc, bt, lens = random_case([L, L // 2 + 1], seed=L)
+    out = run_decode(q, kc, vc, bt, lens)
+    assert_close_attn(to_np(out), oracle(q, kc, vc, bt, lens, 128 ** -0.5), what=f"L={L}")
+
+
+def test_zero_length_padding_rows():
+    # graph padding rows: ctx 0 and block-table row 0 (graph_pad.py PAD_ROW_BLOCK / PAD_CTX_LEN)
+    q, kc, vc, bt, lens = random_case([0, 5, 0, 300, 1], seed=9)
+    bt[0, :] = 0
+    bt[2, :] = -1
+    out = run_decode(q, kc, vc, bt, lens)
+    got = to_np(out)
+    assert np.all(got[0] == 0) and np.all(got[2] == 0)
+    assert_close_attn(got, oracle(q, kc, vc, bt, lens, 128 ** -0.5), what="padding rows")
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 5, 16])
+def test_split_count_invariance(splits):
+    q, kc, vc, bt, lens = random_case([4096, 1700, 256, 3000], seed=21)
+    base = run_decode(q, kc, vc, bt, lens)
+    out = run_decode(q, kc, vc, bt, lens, num_splits=splits)
+    ref = oracle(q, kc, vc, bt, lens, 128 ** -0.5)
+    assert_close_attn(to_np(out), ref, what=f"splits={splits}")
+    # only the fp32 summation order differs: within one bf16 unit of the default plan
+    diff = np.abs(to_np(out) - to_np(base))
+    assert np.all(diff <= 2.0 ** -7 * np.abs(to_np(base)) + 1e-5)
+
+
+@pytest.mark.parametrize("bs", [16, 32, 64, 128, 512])
+def test_page_sizes(bs):
+    q, kc, vc, bt, lens = random_case([1, 100, 777, 2050], bs=bs, seed=bs)
+    out = run_decode(q, kc, vc, bt, lens)
+    assert_close_attn(to_np(out), oracle(q, kc, vc, bt, lens, 128 ** -0.5), what=f"bs={bs}")
+
+
+def test_head_major_pages():
+    q, kc, vc, bt, lens = random_case([513, 1500], seed=31)
+    kh = kc.transpose(1, 2).contiguous()  # (blocks, Hkv, bs, D)
+    vh = vc.transpose(1, 2).contiguous()
+    out = ops.paged_attention(q, kh, vh, bt.to(DEV), 128 ** -0.5, context_lens=lens.to(DEV),
+                              layout="head_major")
+    assert_close_attn(to_np(out), oracle(q, kc, vc, bt, lens, 128 ** -0.5), what="head_major")
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (32, 4), (8, 8), (64, 8), (32, 1)])
+def test_gqa_ratios(hq, hkv):
+    q, kc, vc, bt, lens = random_case([700, 2000, 33], hq=hq, hkv=hkv, seed=hq * 100 + hkv)
+    out = run_decode(q, kc, vc, bt, lens)
+    assert_close_attn(to_np(out), oracle(q, kc, vc, bt, lens, 128 ** -0.5),
+                      what=f"hq={hq} hkv={hkv}")
+
+
+def test_fp16():
+    q, kc, vc, bt, lens = random_case([1234, 4000], dtype=torch.float16, seed=41)
+    out = run_decode(q, kc, vc, bt, lens)
+    assert_close_attn(to_np(out), oracle(q, kc, vc, bt, lens, 128 ** -0.5), what="fp16")
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8)])
+def test_verify_ragged_rows(hq, hkv):
+    # rows per sequence 1..7; one sequence has fewer keys than rows
+    nq = [1, 7, 3, 5, 7, 4]
+    keys = [900, 2600, 3, 257, 1, 40]
+    lens = torch.tensor(keys, dtype=torch.int32)
+    g = torch.Generator().manual_seed(77)
+    bt = workloads.block_tables_for(keys, 256, 40, g, 12)[0]
+    dg = workloads.device_generator(DEV, 78)
+    kc = torch.randn((40, 256, hkv, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    vc = torch.randn((40, 256, hkv, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(nq)]), dtype=torch.int32)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(keys)]), dtype=torch.int32)
+    q = torch.randn((int(cu_q[-1]), hq, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    out = ops.paged_attention(q, kc, vc, bt.to(DEV), 128 ** -0.5, cu_seqlens_k=cu_k.to(DEV),
+                              cu_seqlens_q=cu_q.to(DEV), max_seqlen_q=max(nq))
+    ref = oracle(q, kc, vc, bt, lens, 128 ** -0.5, cu_q)
+    assert_close_attn(to_np(out), ref, what="ragged verify")
+
+
+def test_placement_and_width_invariance_bitwise():
+    # same sequence data at different pages, with a wider -1 padded table
+    q, kc, vc, bt, lens = random_case([1500, 700], seed=51, spare=20)
+    out1 = run_decode(q, kc, vc, bt, lens)
+    used = sorted(set(int(x) for x in bt.flatten().tolist() if x >= 0))
+    free = [p for p in range(kc.shape[0]) if p not in used]
+    move = {p: free[i] for i, p in enumerate(used)}
+    kc2, vc2 = kc.clone(), vc.clone()
+    for p, n in move.items():
+        kc2[n] = kc[p]
+        vc2[n] = vc[p]
+    bt2 = torch.full((bt.shape[0], bt.shape[1] + 9), -1, dtype=torch.int32)
+    for b in range(bt.shape[0]):
+        for j in range(bt.shape[1]):
+            if int(bt[b, j]) >= 0:
+                bt2[b, j] = move[int(bt[b, j])]
+    out2 = run_decode(q, kc2, vc2, bt2, lens)
+    assert torch.equal(out1, out2)
+
+
+def test_repeat_is_bitwise_deterministic():
+    q, kc, vc, bt, lens = random_case([3000, 257, 4096], seed=61)
+    a = run_decode(q, kc, vc, bt, lens)
+    for _ in range(5):
+        assert torch.equal(a, run_decode(q, kc, vc, bt, lens))
+
+
+def test_hip_graph_replay_matches_eager():
+    case = workloads.decode_case(8, seed=71, num_blocks=256, sets=2)
+    kc, vc = case["k_cache"], case["v_cache"]
+    q = case["q"].clone()
+    knew, vnew = case["k_new"].clone(), case["v_new"].clone()
+    bt = case["tables"][0].to(DEV)
+    lens = case["lens"].to(DEV)
+    slots = case["slots"][0].to(DEV)
+    out = torch.empty_like(q)
+    # warm up on a side stream, then capture store + attention
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.store_kvcache(knew, vnew, kc, vc, slots)
+        ops.paged_attention(q, kc, vc, bt, case["scale"], context_lens=lens, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.store_kvcache(knew, vnew, kc, vc, slots)
+        ops.paged_attention(q, kc, vc, bt, case["scale"], context_lens=lens, out=out)
+    for rep, tbl in enumerate([case["tables"][0], case["tables"][1], case["tables"][0]]):
+        dg = workloads.device_generator(DEV, 1000 + rep)
+        q.copy_(torch.randn(q.shape, generator=dg, device=DEV).to(q.dtype))
+        knew.copy_(torch.randn(knew.shape, generator=dg, device=DEV).to(knew.dtype))
+        bt.copy_(tbl.to(DEV))
+        slots.copy_(workloads.slots_for(tbl, [[int(L) - 1] for L in case["lens"]], 256).to(DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        torch.cuda.synchronize()
+        eager = ops.paged_attention(q, kc, vc, bt, case["scale"], context_lens=lens)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager), f"replay {rep} differs from eager"
+        assert_close_attn(to_np(got), oracle(q, kc, vc, tbl, case["lens"], case["scale"]),
+                          what=f"graph replay {rep}")
+
+
+# ------------------------------------------------------------- mirror entry points
+def test_mirror_entry_points_agree():
+    q, kc, vc, bt, lens = random_case([1000, 2500, 1], seed=81)
+    btd, ld = bt.to(DEV), lens.to(DEV)
+    base = run_decode(q, kc, vc, bt, lens)
+    for version in (1, 2, 3):
+        assert torch.equal(paged_decode_attention(q, kc, vc, btd, ld, 128 ** -0.5,
+                                                  version=version), base)
+    assert torch.equal(paged_decode_attention_cuda(q, kc, vc, btd, ld, 128 ** -0.5), base)
+    fa = flash_attn_with_kvcache(q.unsqueeze(1), kc, vc, cache_seqlens=ld, block_table=btd,
+                                 softmax_scale=128 ** -0.5, causal=True)
+    assert fa.shape == (3, 1, 32, 128) and torch.equal(fa[:, 0], base)
+    # Attention module, decode branch (store then attend)
+    attn = Attention(32, 128, 128 ** -0.5, 8)
+    attn.k_cache, attn.v_cache = kc, vc
+    knew = torch.randn((3, 8, 128), device=DEV).to(torch.bfloat16)
+    slots = torch.full((3,), -1, dtype=torch.int32, device=DEV)  # no write: compare to base
+    set_context(False, slot_mapping=slots, context_lens=ld, block_tables=btd)
+    try:
+        o = attn(q, knew, knew)
+    finally:
+        reset_context()
+    assert o.shape == (3, 1, 32, 128) and torch.equal(o[:, 0], base)
+
+
+def test_attention_module_verify_branch():
+    case = workloads.verify_case(seed=91, num_blocks=256)
+    kc, vc = case["k_cache"], case["v_cache"]
+    attn = Attention(32, 128, case["scale"], 8)
+    attn.k_cache, attn.v_cache = kc, vc
+    set_context(True, case["cu_q"].to(DEV), case["cu_k"].to(DEV), case["k"] + 1,
+                int(case["keys"].max()), case["slots"].to(DEV), None, case["table"].to(DEV),
+                is_spec_verify=True)
+    try:
+        o = attn(case["q"], case["k_new"], case["v_new"])
+    finally:
+        reset_context()
+    torch.cuda.synchronize()
+    ref = oracle(case["q"], kc, vc, case["table"], case["keys"], case["scale"], case["cu_q"])
+    assert_close_attn(to_np(o), ref, what="Attention verify")
+    o2 = flash_attn_varlen_func(case["q"], kc, vc, case["cu_q"].to(DEV), case["cu_k"].to(DEV),
+                                case["k"] + 1, int(case["keys"].max()),
+                                softmax_scale=case["scale"], causal=True,
+                                block_table=case["table"].to(DEV))
+    assert torch.equal(o, o2)
+
+
+def test_errors_match_reference_kinds():
+    q, kc, vc, bt, lens = random_case([10], seed=3)
+    btd, ld = bt.to(DEV), lens.to(DEV)
+    with pytest.raises(ValueError):  # paged_decode_attn.py:467-468
+        paged_decode_attention(q, kc, vc, btd, ld, 0.1, version=4)
+    with pytest.raises(AssertionError):  # GQA divisibility, paged_decode_attn.py:384
+        paged_decode_attention(q[:, :30], kc, vc, btd, ld, 0.1)
+    with pytest.raises(RuntimeError):  # unsupported head_dim (TORCH_CHECK kind)
+        q64, k64, v64, bt64, l64 = random_case([10], d=64, seed=4)
+        run_decode(q64, k64, v64, bt64, l64)
+    with pytest.raises(RuntimeError):  # CPU tensors: no fallback
+        ops.paged_attention(q.cpu(), kc.cpu(), vc.cpu(), bt, 0.1, context_lens=lens)

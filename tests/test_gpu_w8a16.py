@@ -1,0 +1,141 @@
+"""GPU parity of the W8A16 fused-dequantization linear against float64
+dequantize-then-matmul (nanovllm/layers/quant.py:151-159,209-223).
+
+Tolerance: the fused kernel rounds only at the 16-bit output, so
+    |y - ref| <= r |ref| + 2^-17 * (|x| @ |w|^T * s)             (elementwise)
+with r = 2^-9 for fp16 output and 2^-8 for bf16 output (twice the half-ulp
+output rounding, plus fp32 accumulation slack), and
+max|y - ref| / max|ref| <= 2e-3 (fp16) or 4e-3 (bf16; the reference reports
+0.3-0.4 % for its bf16 output, docs/W8A16量化-开发记录.md:272-274).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_np
+from oracle import w8a16 as ow8
+from specdec_nanovllm_amd import ops, workloads
+from specdec_nanovllm_amd.layers.linear import ReplicatedLinear
+from specdec_nanovllm_amd.layers.quant import apply_int8_quant, int8_linear, quantize_weight
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def check(y, x, w, s, bias=None, gran="per_channel", gs=128, out_rel=2.0 ** -9, what=""):
+    xn, wn, sn = to_np(x).astype(np.float64), to_np(w), to_np(s).astype(np.float64)
+    bn = None if bias is None else to_np(bias).astype(np.float64)
+    ref = ow8.int8_linear(xn, wn, sn, bn, gran, gs)
+    mag = np.abs(xn) @ np.abs(ow8.dequantize_weight(wn, sn, gran, gs)).T
+    got = to_np(y).astype(np.float64)
+    bound = out_rel * np.abs(ref) + 2.0 ** -17 * mag + 1e-30
+    excess = np.abs(got - ref) - bound
+    assert excess.max() <= 0, f"{what}: max excess {excess.max():.3g}"
+    rel = np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+    rel_max = 2e-3 if y.dtype == torch.float16 else 4e-3
+    assert rel <= rel_max, f"{what}: max|y-ref|/max|ref| = {rel:.3g}"
+
+
+@pytest.mark.parametrize("name,N,K", workloads.W8A16_SHAPES)
+@pytest.mark.parametrize("M", workloads.W8A16_MS)
+def test_c4_shapes_fp16(name, N, K, M):
+    c = workloads.w8a16_case(M, N, K, seed=N + K + M)
+    y = ops.w8a16_linear(c["x"], c["w"], c["s"])
+    assert y.shape == (M, N) and y.dtype == torch.float16
+    check(y, c["x"], c["w"], c["s"], what=f"{name} M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 7, 16, 56])
+def test_bf16_activations_and_scales(M):
+    c = workloads.w8a16_case(M, 6144, 1024, seed=M, act_dtype=torch.bfloat16,
+                             scale_dtype=torch.bfloat16)
+    y = ops.w8a16_linear(c["x"], c["w"], c["s"])
+    assert y.dtype == torch.bfloat16
+    check(y, c["x"], c["w"], c["s"], out_rel=2.0 ** -8, what=f"bf16 M={M}")
+
+
+@pytest.mark.parametrize("gs", [64, 128, 256])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_per_group(gs, act):
+    M, N, K = 5, 1024, 2048
+    c = workloads.w8a16_case(M, N, K, seed=gs, act_dtype=act)
+    g = workloads.device_generator(DEV, 5)
+    s = (torch.rand((N, K // gs), generator=g, device=DEV) * 3e-3 + 1e-3).to(act)
+    y = ops.w8a16_linear(c["x"], c["w"], s, group_size=gs)
+    check(y, c["x"], c["w"], s, gran="per_group", gs=gs,
+          out_rel=2.0 ** -9 if act == torch.float16 else 2.0 ** -8, what=f"group {gs}")
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 1000, 1024), (100, 512, 256), (33, 4096, 64),
+                                   (1, 16, 64), (2, 17, 128), (64, 3072, 1024)])
+def test_ragged_shapes_and_bias(M, N, K):
+    c = workloads.w8a16_case(M, N, K, seed=M * N)
+    bias = torch.randn((N,), device=DEV).to(torch.float16)
+    y = ops.w8a16_linear(c["x"], c["w"], c["s"], bias)
+    check(y, c["x"], c["w"], c["s"], bias, what=f"{M}x{N}x{K}")
+
+
+def test_full_int8_range_including_minus_128():
+    M, N, K = 4, 256, 512
+    w = torch.arange(N * K, device=DEV).remainder(256).sub(128).to(torch.int8).view(N, K)
+    s = torch.full((N,), 1e-3, device=DEV).to(torch.float16)
+    x = torch.randn((M, K), device=DEV).to(torch.float16)
+    check(ops.w8a16_linear(x, w, s), x, w, s, what="full int8 range")
+    xb = x.to(torch.bfloat16)
+    check(ops.w8a16_linear(xb, w, s.to(torch.bfloat16)), xb, w, s.to(torch.bfloat16),
+          out_rel=2.0 ** -8, what="full int8 range bf16")
+
+
+def test_identity_weight_returns_scaled_input():
+    K = 256
+    w = (torch.eye(K, device=DEV) * 100).to(torch.int8)
+    s = torch.full((K,), 0.01, device=DEV).to(torch.float32)
+    x = torch.randn((3, K), device=DEV).to(torch.float16)
+    y = ops.w8a16_linear(x, w, s)
+    # y = x * (100 * 0.01) up to the scale's fp32 rounding and the fp16 output rounding
+    np.testing.assert_allclose(to_np(y), to_np(x), rtol=2.0 ** -10, atol=0)
+
+
+def test_leading_dims_and_mirror_int8_linear():
+    c = workloads.w8a16_case(6, 4096, 1024, seed=9, act_dtype=torch.bfloat16,
+                             scale_dtype=torch.bfloat16)
+    x3 = c["x"].view(2, 3, 1024)
+    y = int8_linear(x3, c["w"], c["s"])
+    assert y.shape == (2, 3, 4096)
+    assert torch.equal(y.view(6, 4096), ops.w8a16_linear(c["x"], c["w"], c["s"]))
+    y2 = int8_linear(x3, c["w"], c["s"], out_features=1000)
+    assert torch.equal(y2.view(6, 1000), y.view(6, 4096)[:, :1000])
+
+
+def test_linear_dispatch_after_apply_int8_quant():
+    torch.manual_seed(0)
+    lin = ReplicatedLinear(1024, 3072).to(DEV)
+    lin.weight.data = (torch.randn((3072, 1024), device=DEV) * 0.02).to(torch.bfloat16)
+    model = torch.nn.Sequential()
+    model.add_module("down", lin)
+    x = torch.randn((7, 1024), device=DEV).to(torch.bfloat16)
+    w_bf16 = lin.weight.data.clone()
+    report = apply_int8_quant(model, ["down"])
+    assert report[0]["shape"] == [3072, 1024] and lin.weight.dtype == torch.int8
+    q, s = quantize_weight(w_bf16)
+    assert torch.equal(lin.weight, q) and torch.equal(lin.weight_scale, s)
+    y = lin(x)
+    check(y, x, lin.weight, lin.weight_scale, out_rel=2.0 ** -8, what="LinearBase int8")
+    lin.to(DEV)  # nn.Module._apply still works on the module
+
+
+def test_split_plans_are_deterministic():
+    c = workloads.w8a16_case(1, 1024, 3072, seed=2)
+    a = ops.w8a16_linear(c["x"], c["w"], c["s"])
+    for _ in range(3):
+        assert torch.equal(a, ops.w8a16_linear(c["x"], c["w"], c["s"]))
+
+
+def test_errors():
+    c = workloads.w8a16_case(1, 64, 96, seed=1)
+    with pytest.raises(RuntimeError):  # K % 64 != 0 is not supported
+        ops.w8a16_linear(c["x"], c["w"], c["s"])
+    with pytest.raises(AssertionError):
+        ops.w8a16_linear(c["x"], c["w"].float(), c["s"])
+    with pytest.raises(RuntimeError):  # CPU tensors: no fallback
+        ops.w8a16_linear(c["x"].cpu(), c["w"].cpu(), c["s"].cpu())
