@@ -64,9 +64,11 @@ int sd_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride
 
 /*
  * Bytes of fp32 split-KV workspace that sd_paged_attention needs for these
- * sizes (0 is a valid answer when no split is ever used).
+ * sizes on the CURRENT device (the work is divided among a number of
+ * workgroups that follows the device's compute-unit count).
  *   max_ctx     : block_table width * block_size (static bound, no host sync)
- *   num_splits  : maximum KV splits per sequence, 0 = library default
+ *   num_splits  : 0 = library default (one resident set of workgroups shares
+ *                 all keys), n > 0 = about n workgroups per (sequence, kv head)
  */
 size_t sd_paged_attention_workspace_size(int32_t num_seqs, int32_t max_qlen,
                                          int32_t num_q_heads, int32_t num_kv_heads,
@@ -98,8 +100,12 @@ size_t sd_paged_attention_workspace_size(int32_t num_seqs, int32_t max_qlen,
  *            (interleaved or head-major page layouts both work)
  * Supported: head_dim 128, dtype bf16/f16, (num_q_heads/num_kv_heads) *
  * max_qlen <= 32. Page ids are clamped into [0, num_blocks).
- * workspace: >= sd_paged_attention_workspace_size(...) bytes (may be NULL if
- * that is 0). num_splits: maximum splits per sequence, 0 = library default.
+ * workspace: >= sd_paged_attention_workspace_size(...) bytes, 16-byte
+ * aligned, queried on the same device. num_splits: as in that query.
+ * Keys are divided evenly among the workgroups across all (sequence, kv head)
+ * pairs (no host sync: the kernels read context_lens themselves); a second
+ * kernel merges the partial softmax states of pairs that several workgroups
+ * shared and writes zeros for sequences without keys.
  */
 int sd_paged_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                        const void* k_cache, const void* v_cache, int64_t cache_stride_block,
@@ -115,9 +121,10 @@ int sd_paged_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
 
 /*
  * Same arguments as sd_paged_attention, but only the split-KV main kernel
- * runs: `out` receives the rows of sequences that fit in one split and the
- * workspace receives the partial (m, l, acc) of the others. Measurement twin
- * of `paged_decode_cuda_partial` (nanovllm/kernels/paged_decode_attn_cuda.cu:1558-1593).
+ * runs: `out` receives the rows of (sequence, kv head) pairs that one
+ * workgroup covered and the workspace the partial (m, l, acc) of the others;
+ * rows of sequences without keys are left untouched. Measurement twin of
+ * `paged_decode_cuda_partial` (nanovllm/kernels/paged_decode_attn_cuda.cu:1558-1593).
  */
 int sd_paged_attention_partial(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                                const void* k_cache, const void* v_cache,

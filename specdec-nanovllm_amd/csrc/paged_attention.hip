@@ -8,21 +8,29 @@
 // rule of the verify forward (nanovllm/layers/attention.py:64-70,
 // nanovllm/engine/model_runner.py:522-533).
 //
-// Work decomposition (split-KV):
-//   grid  = (max_splits, Hkv, B); one workgroup = 4 wave64s owns `chunk`
-//           tokens of one (sequence, kv head) and walks them in tiles of
-//           4 * TPW tokens, every wave taking its own TPW-token slice.
-//   wave  : loads its whole slice up front with 16-byte global loads (K in
-//           MFMA operand order, V as full 256-byte rows), then per 32 tokens
-//             S^T = K . Q^T      4 x MFMA 16x16x32 per 16 tokens per row tile
+// Work decomposition (stream-K over keys):
+//   A "pair" is one (sequence b, kv head h); it has ceil(L_b / 128) workgroup
+//   steps of 128 keys. All pairs' steps are laid end to end (b major, h
+//   minor) and the grid's `nwg` workgroups each take one contiguous run of
+//   S = max(ceil(T / nwg), min_steps) steps, so every workgroup streams the
+//   same number of bytes whatever the length mix, with no host sync: each
+//   workgroup derives T and its start from context_lens itself (a wave-wide
+//   scan of the B lengths).
+//   step  : the 4 wave64s of a workgroup take 32 keys each. A wave loads the
+//           next step's K and V rows (16-byte loads) while it computes the
+//           current one (register double buffer), then per 32 keys
+//             S^T = K . Q^T      4 x MFMA 16x16x32 per 16 keys per row tile
 //             online softmax     exp2 domain, row max over lane groups
 //             O^T += V^T . P^T   16 x MFMA per row tile (P split into hi + lo
 //                                16-bit parts), V^T gathered from LDS
 //           The S^T / O^T orientation puts one query row per lane (l % 16),
 //           so the softmax state never moves between lanes.
-//   merge : the four waves' (m, l, acc) meet in LDS; a single-split sequence
-//           writes the normalised output, otherwise the workgroup writes a
-//           partial to the workspace and `paged_attn_combine` merges them.
+//   flush : when a pair ends (or the run does) the four waves' (m, l, acc)
+//           meet in LDS. A pair covered by one workgroup is written out
+//           normalised; otherwise the workgroup writes a partial to slot
+//           (workgroup + pair) of the workspace and `paged_attn_combine`
+//           merges the partials of each pair (that slot is unique: a later
+//           workgroup can only meet a later pair).
 // G * max_qlen query rows are padded to RT tiles of 16 rows (RT = 1: decode
 // with G <= 16 or the 0.6B verify; RT = 2: Qwen3-4B verify with 7 x 4 rows).
 #include <math.h>
@@ -34,11 +42,15 @@ namespace {
 using sd::f32x4;
 using sd::u32x4;
 
-constexpr int kD = 128;         // head_dim
-constexpr int kWaves = 4;       // wave64s per workgroup
+constexpr int kD = 128;                // head_dim
+constexpr int kWaves = 4;              // wave64s per workgroup
 constexpr int kThreads = 256;
-constexpr int kStep = 32;       // tokens per MFMA step of one wave
-constexpr int kVPitch = 136;    // 16-bit elements per LDS row of a V tile (272 B)
+constexpr int kStep = 32;              // keys per wave per workgroup step
+constexpr int kTile = kWaves * kStep;  // keys per workgroup step
+constexpr int kKPitch = 136;  // 16-bit elements per LDS row of a K tile (272 B: b128 reads of
+                              // 16 consecutive rows hit distinct banks)
+constexpr int kVPitch = 144;  // same for a V tile (288 B: transpose reads of 4 x 4 rows hit
+                              // distinct banks)
 
 struct AttnParams {
   const uint16_t* q;
@@ -46,6 +58,7 @@ struct AttnParams {
   const uint16_t* kc;
   const uint16_t* vc;
   int64_t c_sblk, c_spos, c_shead;
+  uint32_t c_spos32;  // c_spos, which the host checks fits 32 bits with room for a page
   int32_t num_blocks;
   int32_t block_size;
   int32_t bs_shift;  // log2(block_size), or -1 when block_size is not a power of two
@@ -57,16 +70,17 @@ struct AttnParams {
   const int32_t* cu_q;  // (B+1,) cumulative query rows, or NULL (one row per sequence)
   int32_t max_qlen;
   int64_t total_q;
+  int32_t num_seqs;
   int32_t G;
   int32_t Hkv;
   float scale_log2;  // softmax scale * log2(e)
   uint16_t* out;
   int64_t o_stok, o_shead;
-  float* ws_ml;   // [B][Hkv][max_splits][rmax][2]  (m in log2 units, l)
-  float* ws_acc;  // [B][Hkv][max_splits][rmax][kD] unnormalised
-  int32_t chunk;  // tokens per split, a multiple of the workgroup tile
-  int32_t max_splits;
-  int32_t rmax;   // G * max_qlen
+  float* ws_ml;       // [slots][rmax][2]  (m in log2 units, l)
+  float* ws_acc;      // [slots][rmax][kD] unnormalised
+  int32_t nwg;        // workgroups the steps are divided among
+  int32_t min_steps;  // lower bound of steps per workgroup
+  int32_t rmax;       // G * max_qlen
 };
 
 struct SeqInfo {
@@ -76,10 +90,16 @@ struct SeqInfo {
   int R;   // G * nq
 };
 
+__device__ __forceinline__ int seq_keys(const AttnParams& p, int b) {
+  const int L = p.ctx ? p.ctx[b] : (p.cu_k[b + 1] - p.cu_k[b]);
+  return min(max(L, 0), p.max_ctx);
+}
+
+__device__ __forceinline__ int steps_of(int L) { return (L + kTile - 1) / kTile; }
+
 __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b) {
   SeqInfo s;
-  int L = p.ctx ? p.ctx[b] : (p.cu_k[b + 1] - p.cu_k[b]);
-  s.L = min(max(L, 0), p.max_ctx);
+  s.L = seq_keys(p, b);
   if (p.cu_q) {
     s.q0 = p.cu_q[b];
     s.nq = min(max(p.cu_q[b + 1] - p.cu_q[b], 0), p.max_qlen);
@@ -89,6 +109,47 @@ __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b) {
   }
   s.R = p.G * s.nq;
   return s;
+}
+
+// Wave-wide sum of Hkv * steps(b) over b in [0, upto) (every lane gets it).
+__device__ int steps_before(const AttnParams& p, int upto) {
+  const int lane = threadIdx.x & 63;
+  int sum = 0;
+  for (int c = 0; c < upto; c += 64) {
+    const int b = c + lane;
+    sum += b < upto ? steps_of(seq_keys(p, b)) : 0;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  return sum * p.Hkv;
+}
+
+// Wave-wide: the sequence holding global step s (0 <= s < total) and the
+// global index of that sequence's first step.
+__device__ void locate(const AttnParams& p, int s, int& b_out, int& first_out) {
+  const int lane = threadIdx.x & 63;
+  int run = 0;
+  for (int c = 0; c < p.num_seqs; c += 64) {
+    const int b = c + lane;
+    const int n = b < p.num_seqs ? steps_of(seq_keys(p, b)) * p.Hkv : 0;
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off);
+      if (lane >= off) incl += t;
+    }
+    const int excl = run + incl - n;
+    const unsigned long long hit = __ballot(n > 0 && excl <= s && s < excl + n);
+    if (hit) {
+      const int src = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+      b_out = c + src;
+      first_out = __shfl(excl, src);
+      return;
+    }
+    run += __shfl(incl, 63);
+  }
+  b_out = p.num_seqs - 1;  // s >= total: callers never ask
+  first_out = run;
 }
 
 // Element offset of key position `tok` (0 <= tok < L) of one sequence.
@@ -116,362 +177,456 @@ __device__ __forceinline__ void store4(uint16_t* dst, f32x4 v, float s) {
 
 template <int RT>
 constexpr int smem_bytes() {
-  constexpr int vtile = kWaves * kStep * kVPitch * 2;
+  constexpr int vtile = kWaves * kStep * (kKPitch + kVPitch) * 2;  // K and V tile per wave
   constexpr int merge = kWaves * RT * 16 * (2 + kD) * 4;
   return vtile > merge ? vtile : merge;
 }
 
-// Zero rows of a sequence that has no keys at all (padding rows, L = 0).
-template <typename T>
-__device__ void write_zero_rows(const AttnParams& p, const SeqInfo& si, int h) {
-  for (int idx = threadIdx.x; idx < si.R * 32; idx += kThreads) {
-    const int row = idx >> 5, d4 = (idx & 31) * 4;
-    const int qi = row / p.G, g = row - qi * p.G;
-    const int64_t qt = si.q0 + qi;
-    if (qt < 0 || qt >= p.total_q) continue;
-    uint16_t* op = p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + d4;
-    *reinterpret_cast<uint2*>(op) = make_uint2(0u, 0u);
-  }
-}
+// One wave's share of one workgroup step: 32 keys of K and of V, lane l
+// holding key 4 r + l/16, dims 8 (l%16) .. +8 of k[r] / v[r] — 16 lanes read one
+// whole 256-byte row, so every load instruction moves four full rows. Both
+// tiles are then transposed through LDS into MFMA operand order.
+struct StepRegs {
+  u32x4 k[8];
+  u32x4 v[8];
+};
 
-// ONE_PAGE: block_size % TPW == 0, so a wave's TPW-token slice never crosses a
+// ONE_PAGE: block_size % 32 == 0, so a wave's 32-key slice never crosses a
 // page and one block-table lookup serves the whole slice.
-template <typename T, int RT, int TPW, bool ONE_PAGE>
-__global__ __launch_bounds__(kThreads) void paged_attn_main(AttnParams p) {
-  constexpr int NS = TPW / kStep;
+// Waves per SIMD the main kernel is built for (VGPR budget 512 / this); the
+// grid holds this many workgroups per compute unit.
+template <int RT>
+constexpr int main_occupancy() { return RT == 1 ? 2 : 1; }
+
+template <typename T, int RT, bool ONE_PAGE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(main_occupancy<RT>())))
+void paged_attn_main(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[smem_bytes<RT>()];
 
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const SeqInfo si = seq_info(p, b);
-  const int start = split * p.chunk;
-  if (start >= si.L) {
-    if (split == 0) write_zero_rows<T>(p, si, h);
-    return;
-  }
-  const int end = min(start + p.chunk, si.L);
-  const int nsplit = (si.L + p.chunk - 1) / p.chunk;
-
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // wave index held in an SGPR: page lookups and page bases stay scalar
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
 
-  // B operand of S^T = K . Q^T: lane holds Q[row = 16 rt + lr][32 s + 8 lg .. +8].
-  u32x4 qop[RT][4];
-  int lim[RT];  // last key position visible to this lane's row (-1: padding row)
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int row = rt * 16 + lr;
-    const int qi = row / p.G, g = row - qi * p.G;
-    const int64_t qt = si.q0 + qi;
-    const bool valid = row < si.R && qt >= 0 && qt < p.total_q;
-    lim[rt] = valid ? si.L - si.nq + qi : -1;
-    const uint16_t* qp =
-        p.q + (valid ? qt * p.q_stok + static_cast<int64_t>(h * p.G + g) * p.q_shead : 0) + lg * 8;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qop[rt][s] = valid ? sd::load16(qp + s * 32) : u32x4{0u, 0u, 0u, 0u};
-  }
+  // ---- this workgroup's run of steps [s0, s1)
+  const int total = __builtin_amdgcn_readfirstlane(steps_before(p, p.num_seqs));
+  const int S = max((total + p.nwg - 1) / p.nwg, p.min_steps);
+  const int s0 = static_cast<int>(blockIdx.x) * S;
+  if (s0 >= total) return;
+  const int s1 = min(s0 + S, total);
+  int b, first;
+  locate(p, s0, b, first);
+  b = __builtin_amdgcn_readfirstlane(b);
+  first = __builtin_amdgcn_readfirstlane(first);
 
+  SeqInfo si = seq_info(p, b);
+  int n = steps_of(si.L);  // steps of every pair of sequence b
+  int h = (s0 - first) / n;
+  int j = s0 - first - h * n;
+  int j_first = j;  // step at which this workgroup entered the current pair
+
+  // ---- per-pair state: Q operand, causal limits, online-softmax state
+  u32x4 qop[RT][4];
+  int lim[RT];  // last key visible to this lane's row (-1: padding row)
   float m_run[RT], l_run[RT];
   f32x4 acc[RT][8];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    m_run[rt] = -INFINITY;
-    l_run[rt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
 
-  uint16_t* vl = reinterpret_cast<uint16_t*>(smem) + wave * (kStep * kVPitch);
-  const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
-  const int64_t hoff = static_cast<int64_t>(h) * p.c_shead;
-  const int last = si.L - 1;
+  auto begin_pair = [&]() {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int row = rt * 16 + lr;
+      const int qi = row / p.G, g = row - qi * p.G;
+      const int64_t qt = si.q0 + qi;
+      const bool valid = row < si.R && qt >= 0 && qt < p.total_q;
+      lim[rt] = valid ? si.L - si.nq + qi : -1;
+      const uint16_t* qp =
+          p.q + (valid ? qt * p.q_stok + static_cast<int64_t>(h * p.G + g) * p.q_shead : 0) +
+          lg * 8;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        qop[rt][s] = valid ? sd::load16(qp + s * 32) : u32x4{0u, 0u, 0u, 0u};
+      m_run[rt] = -INFINITY;
+      l_run[rt] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
 
-  for (int t0 = __builtin_amdgcn_readfirstlane(start + wave * TPW); t0 < end;
-       t0 += kWaves * TPW) {
-    // One page lookup per wave slice when the slice cannot cross a page
-    // (every clamped token stays in [t0, t0 + TPW)); per-lane lookups otherwise.
-    const int64_t base0 = ONE_PAGE ? kv_row(p, btrow, t0) : 0;
-    auto row_of = [&](int tok) -> int64_t {
-      return ONE_PAGE ? base0 + static_cast<int64_t>(tok - t0) * p.c_spos
-                      : kv_row(p, btrow, tok);
-    };
-    // ---- issue every load of this slice before any math
-    u32x4 kr[NS][2][4];
-    u32x4 vr[NS][8];
-#pragma unroll
-    for (int st = 0; st < NS; ++st) {
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int tok = min(t0 + st * kStep + tt * 16 + lr, last);
-        const uint16_t* kp = p.kc + row_of(tok) + hoff + lg * 8;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) kr[st][tt][s] = sd::load16(kp + s * 32);
-      }
+  auto load_step = [&](StepRegs& R, int lb, int lh, int lj, int L) {
+    const int t0 = lj * kTile + wave * kStep;
+    if (t0 >= L) return;  // wave-uniform: this wave has no keys in the step
+    const int last = L - 1;
+    const int32_t* btrow = p.bt + static_cast<int64_t>(lb) * p.bt_stride;
+    const int64_t hoff = static_cast<int64_t>(lh) * p.c_shead;
+    if constexpr (ONE_PAGE) {
+      // scalar page base + 32-bit lane offsets (key rows of one page)
+      const int64_t base = kv_row(p, btrow, t0) + hoff;
+      const char* kpg = reinterpret_cast<const char*>(p.kc + base);
+      const char* vpg = reinterpret_cast<const char*>(p.vc + base);
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        const int tok = min(t0 + st * kStep + r * 4 + lg, last);
-        vr[st][r] = sd::load16(p.vc + row_of(tok) + hoff + lr * 8);
+        const uint32_t off =  // bytes
+            (static_cast<uint32_t>(min(t0 + r * 4 + lg, last) - t0) * p.c_spos32 + lr * 8) * 2u;
+        R.k[r] = sd::load16_stream(kpg + off);
+        R.v[r] = sd::load16_stream(vpg + off);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int64_t off = kv_row(p, btrow, min(t0 + r * 4 + lg, last)) + hoff + lr * 8;
+        R.k[r] = sd::load16_stream(p.kc + off);
+        R.v[r] = sd::load16_stream(p.vc + off);
+      }
+    }
+  };
+
+  uint16_t* kl = reinterpret_cast<uint16_t*>(smem) + wave * (kStep * (kKPitch + kVPitch));
+  uint16_t* vl = kl + kStep * kKPitch;
+
+  auto compute_step = [&](StepRegs& R, int cj) {
+    const int tb = cj * kTile + wave * kStep;
+    if (tb >= si.L) return;
+    // ---- stage the 32 K and V rows of this step (row-major, padded pitch)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      sd::store16(kl + (r * 4 + lg) * kKPitch + lr * 8, R.k[r]);
+      sd::store16(vl + (r * 4 + lg) * kVPitch + lr * 8, R.v[r]);
+    }
+    sd::wave_lds_sync();  // rows written by other lanes of this wave are read below
+    // ---- S^T tiles: lane holds S[row lr][key tb + 16 tt + 4 lg + i]; the K
+    //      A operand of MFMA s is key 16 tt + lr, dims 32 s + 8 lg .. +8
+    f32x4 sc[RT][2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      u32x4 ka[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ka[s] = sd::load16(kl + (tt * 16 + lr) * kKPitch + s * 32 + lg * 8);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) c = sd::Elem<T>::mfma(ka[s], qop[rt][s], c);
+        sc[rt][tt] = c;
       }
     }
 
+    // ---- online softmax; P^T operand: k-slot 8 lg + j <-> key 4 lg + j (j < 4)
+    //      and key 16 + 4 lg + (j - 4) (j >= 4), the order S^T already holds.
+    u32x4 pop[RT], plo[RT];
+    // every row sees every key of this slice: no causal / length mask needed
+    const bool full = tb + kStep - 1 <= si.L - si.nq;
 #pragma unroll
-    for (int st = 0; st < NS; ++st) {
-      const int tb = t0 + st * kStep;
-      // ---- S^T tiles: lane holds S[row lr][token tb + 16 tt + 4 lg + i]
-      f32x4 sc[RT][2];
+    for (int rt = 0; rt < RT; ++rt) {
+      float mloc = -INFINITY;
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
+      for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int s = 0; s < 4; ++s) c = sd::Elem<T>::mfma(kr[st][tt][s], qop[rt][s], c);
-          sc[rt][tt] = c;
+        for (int i = 0; i < 4; ++i) {
+          float s = sc[rt][tt][i] * p.scale_log2;
+          if (!full) {
+            const int tok = tb + tt * 16 + lg * 4 + i;
+            s = (tok <= lim[rt]) ? s : -INFINITY;  // lim < L: also masks keys past the end
+          }
+          sc[rt][tt][i] = s;
+          mloc = fmaxf(mloc, s);
         }
       }
-      // ---- stage the 32 V rows of this step (row-major, padded pitch)
+      mloc = sd::max_over_groups(mloc);
+      const float mnew = fmaxf(m_run[rt], mloc);
+      const float mb = (mnew == -INFINITY) ? 0.f : mnew;
+      float pv[8];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) sd::store16(vl + (r * 4 + lg) * kVPitch + lr * 8, vr[st][r]);
-
-      // ---- online softmax; P^T operand: k-slot 8 lg + j <-> token 4 lg + j (j < 4)
-      //      and token 16 + 4 lg + (j - 4) (j >= 4), the order S^T already holds.
-      u32x4 pop[RT], plo[RT];
+      for (int q = 0; q < 4; ++q) {
+        pv[q] = sd::fast_exp2(sc[rt][0][q] - mb);
+        pv[4 + q] = sd::fast_exp2(sc[rt][1][q] - mb);
+      }
+      float ps = 0.f;
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int tok = tb + tt * 16 + lg * 4 + i;
-            float s = sc[rt][tt][i] * p.scale_log2;
-            s = (tok < end && tok <= lim[rt]) ? s : -INFINITY;
-            sc[rt][tt][i] = s;
-            mloc = fmaxf(mloc, s);
-          }
-        }
-        mloc = sd::max_over_groups(mloc);
-        const float mnew = fmaxf(m_run[rt], mloc);
-        const float mb = (mnew == -INFINITY) ? 0.f : mnew;
-        const float alpha = exp2f(m_run[rt] - mb);
-        float pv[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          pv[j] = exp2f(sc[rt][0][j] - mb);
-          pv[4 + j] = exp2f(sc[rt][1][j] - mb);
-        }
-        float ps = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ps += pv[j];
-        l_run[rt] = l_run[rt] * alpha + ps;
-        m_run[rt] = mnew;
+      for (int q = 0; q < 8; ++q) ps += pv[q];
+      // rescale the running sums only when some row's maximum grew (rare after
+      // the first keys); alpha = 1 for the others
+      if (__any(mnew > m_run[rt])) {
+        const float alpha = sd::fast_exp2(m_run[rt] - mb);
+        l_run[rt] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) acc[rt][dt] *= alpha;
-        // P = hi + lo in two 16-bit operands: P.V keeps ~16 mantissa bits of P
-        // instead of the 8 (bf16) a single rounding would leave.
-        uint32_t hi[4], lo[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sd::split_pack<T>(pv[2 * j], pv[2 * j + 1], hi[j], lo[j]);
-        pop[rt] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-        plo[rt] = u32x4{lo[0], lo[1], lo[2], lo[3]};
       }
+      l_run[rt] += ps;
+      m_run[rt] = mnew;
+      // P = hi + lo in two 16-bit operands: P.V keeps ~16 mantissa bits of P
+      // instead of the 8 (bf16) a single rounding would leave.
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sd::split_pack<T>(pv[2 * q], pv[2 * q + 1], hi[q], lo[q]);
+      pop[rt] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+      plo[rt] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    }
 
-      // ---- O^T += V^T . P^T; A operand lane holds V[token slot][dim 16 dt + lr]
+    // ---- O^T += V^T . P^T; A operand lane holds V[key of slot 8 lg + j][dim 16 dt + lr].
+    //      Two transpose reads: lane lr of block lg addresses key 4 lg + lr / 4 (then
+    //      16 + 4 lg + lr / 4), dims 16 dt + 4 (lr % 4) .. +4, and receives keys
+    //      4 lg .. 4 lg + 3 (then 16 + 4 lg ..) of dim 16 dt + lr.
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const uint16_t* c0 = vl + (lg * 4) * kVPitch + dt * 16 + lr;
-        const uint16_t* c1 = c0 + 16 * kVPitch;
-        u32x4 vop;
-        vop.x = static_cast<uint32_t>(c0[0]) | (static_cast<uint32_t>(c0[kVPitch]) << 16);
-        vop.y = static_cast<uint32_t>(c0[2 * kVPitch]) | (static_cast<uint32_t>(c0[3 * kVPitch]) << 16);
-        vop.z = static_cast<uint32_t>(c1[0]) | (static_cast<uint32_t>(c1[kVPitch]) << 16);
-        vop.w = static_cast<uint32_t>(c1[2 * kVPitch]) | (static_cast<uint32_t>(c1[3 * kVPitch]) << 16);
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint16_t* c = vl + (lg * 4 + (lr >> 2)) * kVPitch + dt * 16 + (lr & 3) * 4;
+      const uint2 v0 = sd::lds_read_tr16(c);
+      const uint2 v1 = sd::lds_read_tr16(c + 16 * kVPitch);
+      const u32x4 vop = {v0.x, v0.y, v1.x, v1.y};
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          acc[rt][dt] = sd::Elem<T>::mfma(vop, pop[rt], acc[rt][dt]);
-          acc[rt][dt] = sd::Elem<T>::mfma(vop, plo[rt], acc[rt][dt]);
+      for (int rt = 0; rt < RT; ++rt) {
+        acc[rt][dt] = sd::Elem<T>::mfma(vop, pop[rt], acc[rt][dt]);
+        acc[rt][dt] = sd::Elem<T>::mfma(vop, plo[rt], acc[rt][dt]);
+      }
+    }
+    sd::wave_lds_sync();  // every lane has read the tile before the next step overwrites it
+  };
+
+  // Merge the four waves' state of the current pair in LDS and write it out:
+  // normalised rows if this workgroup saw the whole pair, else a partial.
+  auto flush = [&](bool complete) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) l_run[rt] = sd::sum_over_groups(l_run[rt]);
+    __syncthreads();  // every wave is done with its V tile; reuse LDS
+    float* mm = reinterpret_cast<float*>(smem);
+    float* ml = mm + kWaves * RT * 16;
+    float* ma = ml + kWaves * RT * 16;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int row = rt * 16 + lr;
+      const int slot = wave * RT * 16 + row;
+      if (lg == 0) {
+        mm[slot] = m_run[rt];
+        ml[slot] = l_run[rt];
+      }
+      if (row < si.R) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+          sd::store16(ma + slot * kD + dt * 16 + lg * 4, __builtin_bit_cast(u32x4, acc[rt][dt]));
+      }
+    }
+    __syncthreads();
+    const int nrows = min(si.R, RT * 16);
+    const int64_t wslot = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(b) * p.Hkv + h;
+    for (int idx = tid; idx < nrows * 32; idx += kThreads) {
+      const int row = idx >> 5, d4 = (idx & 31) * 4;
+      const int qi = row / p.G, g = row - qi * p.G;
+      const int64_t qt = si.q0 + qi;
+      if (qt < 0 || qt >= p.total_q) continue;
+      float mw[kWaves];
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        mw[w] = mm[w * RT * 16 + row];
+        M = fmaxf(M, mw[w]);
+      }
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+      float l = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const float e = exp2f(mw[w] - M);
+          l += e * ml[w * RT * 16 + row];
+          o += e * __builtin_bit_cast(f32x4, sd::load16(ma + (w * RT * 16 + row) * kD + d4));
+        }
+      }
+      if (complete) {
+        uint16_t* op =
+            p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + d4;
+        store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);
+      } else {
+        const int64_t e = wslot * p.rmax + row;
+        sd::store16(p.ws_acc + e * kD + d4, __builtin_bit_cast(u32x4, o));
+        if ((idx & 31) == 0) {
+          p.ws_ml[2 * e] = M;
+          p.ws_ml[2 * e + 1] = l;
         }
       }
     }
-  }
+    __syncthreads();  // LDS is V tiles again
+  };
 
-  // ---- merge the four waves of this workgroup in LDS
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) l_run[rt] = sd::sum_over_groups(l_run[rt]);
-  __syncthreads();  // every wave is done with its V tile; reuse LDS
-  float* mm = reinterpret_cast<float*>(smem);
-  float* ml = mm + kWaves * RT * 16;
-  float* ma = ml + kWaves * RT * 16;
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int row = rt * 16 + lr;
-    const int slot = wave * RT * 16 + row;
-    if (lg == 0) {
-      mm[slot] = m_run[rt];
-      ml[slot] = l_run[rt];
-    }
-    if (row < si.R) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-        sd::store16(ma + slot * kD + dt * 16 + lg * 4, __builtin_bit_cast(u32x4, acc[rt][dt]));
-    }
-  }
-  __syncthreads();
-
-  const int nrows = min(si.R, RT * 16);
-  for (int idx = tid; idx < nrows * 32; idx += kThreads) {
-    const int row = idx >> 5, d4 = (idx & 31) * 4;
-    const int qi = row / p.G, g = row - qi * p.G;
-    const int64_t qt = si.q0 + qi;
-    if (qt < 0 || qt >= p.total_q) continue;
-    float mw[kWaves];
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      mw[w] = mm[w * RT * 16 + row];
-      M = fmaxf(M, mw[w]);
-    }
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    float l = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float e = exp2f(mw[w] - M);
-        l += e * ml[w * RT * 16 + row];
-        o += e * __builtin_bit_cast(f32x4, sd::load16(ma + (w * RT * 16 + row) * kD + d4));
+  // ---- walk [s0, s1): load step s + 1 while computing step s
+  begin_pair();
+  StepRegs ra, rb;
+  load_step(ra, b, h, j, si.L);
+  int s = s0;
+  auto advance = [&](StepRegs& cur, StepRegs& nxt) -> bool {
+    // position of step s + 1
+    int nb = b, nh = h, nj = j + 1;
+    int nL = si.L;
+    const bool more = s + 1 < s1;
+    if (more) {
+      if (nj == n) {
+        nj = 0;
+        if (++nh == p.Hkv) {
+          nh = 0;
+          do {
+            ++nb;
+            nL = seq_keys(p, nb);
+          } while (nL == 0);  // sequences without keys own no steps; s + 1 < total ends the scan
+        }
       }
+      load_step(nxt, nb, nh, nj, nL);
     }
-    if (nsplit == 1) {
-      uint16_t* op = p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + d4;
-      store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);
-    } else {
-      const int64_t e =
-          ((static_cast<int64_t>(b) * p.Hkv + h) * p.max_splits + split) * p.rmax + row;
-      sd::store16(p.ws_acc + e * kD + d4, __builtin_bit_cast(u32x4, o));
-      if ((idx & 31) == 0) {
-        p.ws_ml[2 * e] = M;
-        p.ws_ml[2 * e + 1] = l;
+    compute_step(cur, j);
+    const bool pair_end = j + 1 == n;
+    if (pair_end || !more) flush(pair_end && j_first == 0);
+    if (!more) return false;
+    if (nb != b || nh != h) {
+      if (nb != b) {
+        b = nb;
+        si = seq_info(p, b);
+        n = steps_of(si.L);
       }
+      h = nh;
+      j_first = 0;
+      begin_pair();
     }
+    j = nj;
+    ++s;
+    return true;
+  };
+  for (;;) {
+    if (!advance(ra, rb)) break;
+    if (!advance(rb, ra)) break;
   }
 }
 
-// Log-sum-exp merge of the split partials of one (sequence, kv head). The
-// split loops move kUnroll partials per iteration with every load issued
-// before any use, so the merge costs a few memory round trips, not one per split.
+// Log-sum-exp merge of the partials of pair (b, h) = (blockIdx.z, blockIdx.y),
+// rows blockIdx.x * 8 .. +8 (one thread per row and 4 dims), zero rows for
+// sequences without keys. The pair spans global steps [f, f + n); the
+// workgroups that met it are f / S .. (f + n - 1) / S and workgroup w wrote
+// its partial to slot w + pair. A pair met by one workgroup is already final.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
-  constexpr int kUnroll = 8;
-  const int h = blockIdx.x, b = blockIdx.y;
+  constexpr int kUnroll = 16;
+  const int h = blockIdx.y, b = blockIdx.z;
   const SeqInfo si = seq_info(p, b);
-  const int nsplit = (si.L + p.chunk - 1) / p.chunk;
-  if (nsplit <= 1) return;
-  const int64_t e0 = (static_cast<int64_t>(b) * p.Hkv + h) * p.max_splits * p.rmax;
-  const int nrows = min(si.R, p.rmax);
+  const int row = blockIdx.x * (kThreads / 32) + (threadIdx.x >> 5);
+  const int d4 = (threadIdx.x & 31) * 4;
+  const int total = steps_before(p, p.num_seqs);
+  const int first_b = steps_before(p, b);
+  if (row >= si.R) return;
+  const int qi = row / p.G, g = row - qi * p.G;
+  const int64_t qt = si.q0 + qi;
+  if (qt < 0 || qt >= p.total_q) return;
+  uint16_t* op = p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + d4;
+  const int n = steps_of(si.L);
+  if (n == 0) {
+    *reinterpret_cast<uint2*>(op) = make_uint2(0u, 0u);
+    return;
+  }
+  const int S = max((total + p.nwg - 1) / p.nwg, p.min_steps);
+  const int f = first_b + h * n;
+  const int w0 = f / S, w1 = (f + n - 1) / S;
+  if (w0 == w1) return;
   const float2* ml = reinterpret_cast<const float2*>(p.ws_ml);
-  for (int idx = threadIdx.x; idx < nrows * 32; idx += kThreads) {
-    const int row = idx >> 5, d4 = (idx & 31) * 4;
-    const int qi = row / p.G, g = row - qi * p.G;
-    const int64_t qt = si.q0 + qi;
-    if (qt < 0 || qt >= p.total_q) continue;
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < nsplit; s0 += kUnroll) {
-      float mv[kUnroll];
+  const int64_t base =
+      (static_cast<int64_t>(w0) + static_cast<int64_t>(b) * p.Hkv + h) * p.rmax + row;
+  const int cnt = w1 - w0 + 1;
+  float M = -INFINITY;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  float l = 0.f;
+  for (int c0 = 0; c0 < cnt; c0 += kUnroll) {
+    float2 part[kUnroll];
+    f32x4 a[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-        mv[u] = s0 + u < nsplit ? ml[e0 + (s0 + u) * p.rmax + row].x : -INFINITY;
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) M = fmaxf(M, mv[u]);
-    }
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    float l = 0.f;
-    if (M != -INFINITY) {
-      for (int s0 = 0; s0 < nsplit; s0 += kUnroll) {
-        float2 part[kUnroll];
-        f32x4 acc[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int64_t e = e0 + (s0 + u) * p.rmax + row;
-          if (s0 + u < nsplit) {
-            part[u] = ml[e];
-            acc[u] = __builtin_bit_cast(f32x4, sd::load16(p.ws_acc + e * kD + d4));
-          } else {
-            part[u] = make_float2(-INFINITY, 0.f);
-            acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const float w = exp2f(part[u].x - M);
-          l += w * part[u].y;
-          o += w * acc[u];
-        }
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t e = base + static_cast<int64_t>(c0 + u) * p.rmax;
+      if (c0 + u < cnt) {
+        part[u] = ml[e];
+        a[u] = __builtin_bit_cast(f32x4, sd::load16(p.ws_acc + e * kD + d4));
+      } else {
+        part[u] = make_float2(-INFINITY, 0.f);
+        a[u] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
-    uint16_t* op = p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + d4;
-    store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);
+    float mc = M;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) mc = fmaxf(mc, part[u].x);
+    if (mc == -INFINITY) continue;
+    const float r = exp2f(M - mc);  // rescale what earlier batches summed
+    l *= r;
+    o *= r;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const float w = exp2f(part[u].x - mc);
+      l += w * part[u].y;
+      o += w * a[u];
+    }
+    M = mc;
   }
+  store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);
 }
 
 // ------------------------------------------------------------------ host
 struct Plan {
-  int RT;          // 16-row tiles of query rows
-  int TPW;         // tokens per wave per tile
-  int chunk;       // tokens per split
-  int max_splits;  // grid.x
-  int rmax;        // rows per (sequence, kv head) in the workspace
+  int RT;         // 16-row tiles of query rows
+  int nwg;        // workgroups of the main grid
+  int min_steps;  // lower bound of steps per workgroup
+  int rmax;       // rows per (sequence, kv head) in the workspace
+  int64_t slots;  // partial slots: nwg + num_seqs * Hkv
 };
 
-Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int64_t max_ctx, int num_splits) {
+// Compute units of the current device (cached per device id).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0)
+    n = 256;
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
+}
+
+// num_splits == 0: one resident set of workgroups (main_occupancy per compute
+// unit) shares all the steps.
+// num_splits > 0: num_splits workgroups per (sequence, kv head) on average,
+// the meaning of the reference's `splits` (KV splits per sequence).
+Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   Plan pl;
   const int G = Hq / Hkv;
   pl.rmax = G * max_qlen;
   pl.RT = pl.rmax <= 16 ? 1 : 2;
-  pl.TPW = 64;
-  if (pl.RT == 2) pl.TPW = 32;
-  // Small batches: halve the tile so the grid still covers the 256 CUs.
-  const int64_t tiles256 = (max_ctx + 255) / 256;
-  if (static_cast<int64_t>(num_seqs) * Hkv * tiles256 < 1024) pl.TPW = 32;
-  const int tile = kWaves * pl.TPW;
-  int64_t chunk = tile;
   if (num_splits > 0) {
-    const int64_t per = (max_ctx + num_splits - 1) / num_splits;
-    chunk = (per + tile - 1) / tile * tile;
-    if (chunk < tile) chunk = tile;
+    const int64_t w = static_cast<int64_t>(num_splits) * num_seqs * Hkv;
+    pl.nwg = static_cast<int>(w < (1 << 20) ? w : (1 << 20));
+    pl.min_steps = 1;
+  } else {
+    pl.nwg = device_cus() * (pl.RT == 1 ? main_occupancy<1>() : main_occupancy<2>());
+    pl.min_steps = pl.RT == 1 ? 1 : 2;
   }
-  pl.chunk = static_cast<int>(chunk);
-  int64_t ms = (max_ctx + chunk - 1) / chunk;
-  pl.max_splits = static_cast<int>(ms < 1 ? 1 : ms);
+  pl.slots = static_cast<int64_t>(pl.nwg) + static_cast<int64_t>(num_seqs) * Hkv;
   return pl;
 }
 
-size_t ws_bytes(const Plan& pl, int num_seqs, int Hkv) {
-  if (pl.max_splits <= 1) return 0;
-  const size_t entries = static_cast<size_t>(num_seqs) * Hkv * pl.max_splits * pl.rmax;
-  const size_t ml = (entries * 2 * sizeof(float) + 255) / 256 * 256;
-  return ml + entries * kD * sizeof(float);
+size_t ml_bytes(const Plan& pl) {
+  return (static_cast<size_t>(pl.slots) * pl.rmax * 2 * sizeof(float) + 255) / 256 * 256;
 }
 
-template <typename T, int RT, int TPW>
-void launch_main(const AttnParams& p, dim3 grid, hipStream_t st) {
-  if (p.block_size % TPW == 0)
-    hipLaunchKernelGGL((paged_attn_main<T, RT, TPW, true>), grid, dim3(kThreads), 0, st, p);
+size_t ws_bytes(const Plan& pl) {
+  return ml_bytes(pl) + static_cast<size_t>(pl.slots) * pl.rmax * kD * sizeof(float);
+}
+
+template <typename T, int RT>
+void launch_main(const AttnParams& p, hipStream_t st) {
+  if (p.block_size % kStep == 0)
+    hipLaunchKernelGGL((paged_attn_main<T, RT, true>), dim3(p.nwg), dim3(kThreads), 0, st, p);
   else
-    hipLaunchKernelGGL((paged_attn_main<T, RT, TPW, false>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((paged_attn_main<T, RT, false>), dim3(p.nwg), dim3(kThreads), 0, st, p);
 }
 
 template <typename T>
-int launch_all(const AttnParams& p, const Plan& pl, int num_seqs, bool combine, hipStream_t st) {
-  const dim3 grid(pl.max_splits, p.Hkv, num_seqs);
-  if (pl.RT == 1) {
-    if (pl.TPW == 64) launch_main<T, 1, 64>(p, grid, st);
-    else launch_main<T, 1, 32>(p, grid, st);
-  } else {
-    launch_main<T, 2, 32>(p, grid, st);
-  }
+int launch_all(const AttnParams& p, const Plan& pl, bool combine, hipStream_t st) {
+  if (pl.RT == 1) launch_main<T, 1>(p, st);
+  else launch_main<T, 2>(p, st);
   int rc = sd::check_launch("paged_attention main");
-  if (rc != SD_OK || !combine || pl.max_splits <= 1) return rc;
-  hipLaunchKernelGGL((paged_attn_combine<T>), dim3(p.Hkv, num_seqs), dim3(kThreads), 0, st, p);
+  if (rc != SD_OK || !combine) return rc;
+  const dim3 grid((pl.rmax + kThreads / 32 - 1) / (kThreads / 32), p.Hkv, p.num_seqs);
+  hipLaunchKernelGGL((paged_attn_combine<T>), grid, dim3(kThreads), 0, st, p);
   return sd::check_launch("paged_attention combine");
 }
 
@@ -540,9 +695,21 @@ int run_attention(bool combine, const void* q, int64_t q_stride_tok, int64_t q_s
                   "aligned");
     return SD_ERR_UNSUPPORTED;
   }
-  const Plan pl = make_plan(num_seqs, max_qlen, num_q_heads, num_kv_heads, max_ctx, num_splits);
-  const size_t need = ws_bytes(pl, num_seqs, num_kv_heads);
-  if (need > 0 && (!workspace || workspace_bytes < need || !sd::aligned16(workspace))) {
+  if (cache_stride_block < 0 || cache_stride_pos < 0 || cache_stride_head < 0 ||
+      cache_stride_pos > (1ll << 25)) {
+    sd::set_error("paged_attention: cache strides must be non-negative and the key-row stride "
+                  "at most 2^25 elements");
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (static_cast<int64_t>(num_seqs) * num_kv_heads * ((max_ctx + kTile - 1) / kTile) >
+      (1ll << 30)) {
+    sd::set_error("paged_attention: %d sequences x %d kv heads x %lld keys is too much work "
+                  "for one call", num_seqs, num_kv_heads, (long long)max_ctx);
+    return SD_ERR_UNSUPPORTED;
+  }
+  const Plan pl = make_plan(num_seqs, max_qlen, num_q_heads, num_kv_heads, num_splits);
+  const size_t need = ws_bytes(pl);
+  if (!workspace || workspace_bytes < need || !sd::aligned16(workspace)) {
     sd::set_error("paged_attention: workspace of %zu bytes (16-byte aligned) required, got %zu",
                   need, workspace ? workspace_bytes : (size_t)0);
     return SD_ERR_WORKSPACE;
@@ -557,6 +724,7 @@ int run_attention(bool combine, const void* q, int64_t q_stride_tok, int64_t q_s
   p.c_sblk = cache_stride_block;
   p.c_spos = cache_stride_pos;
   p.c_shead = cache_stride_head;
+  p.c_spos32 = static_cast<uint32_t>(cache_stride_pos);
   p.num_blocks = static_cast<int32_t>(num_blocks);
   p.block_size = block_size;
   p.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
@@ -574,23 +742,16 @@ int run_attention(bool combine, const void* q, int64_t q_stride_tok, int64_t q_s
   p.out = static_cast<uint16_t*>(out);
   p.o_stok = out_stride_tok;
   p.o_shead = out_stride_head;
-  if (need > 0) {
-    const size_t entries =
-        static_cast<size_t>(num_seqs) * num_kv_heads * pl.max_splits * pl.rmax;
-    p.ws_ml = static_cast<float*>(workspace);
-    p.ws_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                        (entries * 2 * sizeof(float) + 255) / 256 * 256);
-  } else {
-    p.ws_ml = nullptr;
-    p.ws_acc = nullptr;
-  }
-  p.chunk = pl.chunk;
-  p.max_splits = pl.max_splits;
+  p.ws_ml = static_cast<float*>(workspace);
+  p.ws_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + ml_bytes(pl));
+  p.num_seqs = num_seqs;
+  p.nwg = pl.nwg;
+  p.min_steps = pl.min_steps;
   p.rmax = pl.rmax;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == SD_BF16) return launch_all<__bf16>(p, pl, num_seqs, combine, st);
-  return launch_all<_Float16>(p, pl, num_seqs, combine, st);
+  if (dtype == SD_BF16) return launch_all<__bf16>(p, pl, combine, st);
+  return launch_all<_Float16>(p, pl, combine, st);
 }
 
 }  // namespace
@@ -603,8 +764,8 @@ extern "C" size_t sd_paged_attention_workspace_size(int32_t num_seqs, int32_t ma
   if (num_seqs <= 0 || max_qlen <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_ctx <= 0 ||
       num_q_heads % num_kv_heads != 0 || num_splits < 0)
     return 0;
-  const Plan pl = make_plan(num_seqs, max_qlen, num_q_heads, num_kv_heads, max_ctx, num_splits);
-  return ws_bytes(pl, num_seqs, num_kv_heads);
+  const Plan pl = make_plan(num_seqs, max_qlen, num_q_heads, num_kv_heads, num_splits);
+  return ws_bytes(pl);
 }
 
 extern "C" int sd_paged_attention(

@@ -65,8 +65,22 @@ __device__ __forceinline__ void split_pack(float a, float b, uint32_t& hi, uint3
 __device__ __forceinline__ u32x4 load16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
+// 16-byte load of data read once (KV cache, weights): the nontemporal hint
+// keeps the stream from displacing reusable lines in the caches.
+__device__ __forceinline__ u32x4 load16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 __device__ __forceinline__ void store16(void* p, u32x4 v) {
   *reinterpret_cast<u32x4*>(p) = v;
+}
+
+// Orders LDS traffic between the lanes of one wave (a wave-private LDS tile
+// written by some lanes and read by others): a compiler barrier plus the
+// wavefront-scope fences of the AMDGPU memory model.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Butterfly max/sum over the four lane groups that share `l % 16`.
@@ -79,6 +93,20 @@ __device__ __forceinline__ float sum_over_groups(float v) {
   v += __shfl_xor(v, 16);
   v += __shfl_xor(v, 32);
   return v;
+}
+
+// 2^x on the transcendental unit (v_exp_f32) without denormal fix-ups:
+// results below 2^-126 flush to 0, 2^-inf = 0. Softmax weights only.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// LDS transpose read (ds_read_b64_tr_b16): within every 16-lane block, lane
+// 4a + c receives 16-bit element c of the 8-byte chunks addressed by lanes
+// a, a + 4, a + 8 and a + 12 of that block, in that order.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(uint2, r);
 }
 
 // --------------------------------------------------------------- host side

@@ -129,12 +129,13 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         return out
     lib = _lib.load()
     max_blocks = bt.shape[1]
-    ws_bytes = lib.sd_paged_attention_workspace_size(
-        num_seqs, int(max_seqlen_q), num_q_heads, num_kv_heads, head_dim,
-        max_blocks * block_size, int(num_splits))
-    ws = _workspace(ws_bytes, dev)
     fn = lib.sd_paged_attention_partial if main_only else lib.sd_paged_attention
     with torch.cuda.device(dev):
+        # the plan (and so the workspace) depends on the device's compute units
+        ws_bytes = lib.sd_paged_attention_workspace_size(
+            num_seqs, int(max_seqlen_q), num_q_heads, num_kv_heads, head_dim,
+            max_blocks * block_size, int(num_splits))
+        ws = _workspace(ws_bytes, dev)
         rc = fn(q.data_ptr(), q.stride(0), q.stride(1),
                 k_cache.data_ptr(), v_cache.data_ptr(), sb, sp, sh, num_blocks,
                 block_size, bt.data_ptr(), bt.stride(0), max_blocks,
