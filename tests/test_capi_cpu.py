@@ -94,11 +94,17 @@ def test_validation_errors_without_gpu():
 
 def test_workspace_queries():
     lib = _lib.load()
-    # C2 B=32: 16 splits of 256 tokens, 4 rows, (m, l) + 128 fp32 per row
-    n = lib.sd_paged_attention_workspace_size(32, 1, 32, 8, 128, 4096, 0)
-    entries = 32 * 8 * 16 * 4
+    # num_splits = 4 at C2 B=32: 4 * 32 * 8 workgroups, one partial slot per
+    # workgroup plus one per (sequence, kv head); 4 rows of (m, l) + 128 fp32 each
+    n = lib.sd_paged_attention_workspace_size(32, 1, 32, 8, 128, 4096, 4)
+    entries = (4 * 32 * 8 + 32 * 8) * 4
     assert n == (entries * 8 + 255) // 256 * 256 + entries * 128 * 4
-    assert lib.sd_paged_attention_workspace_size(1, 1, 32, 8, 128, 128, 0) == 0  # one split
+    # verify rows (7 x 4) widen every slot; the default plan follows the device
+    nv = lib.sd_paged_attention_workspace_size(8, 7, 32, 8, 128, 2816, 4)
+    ev = (4 * 8 * 8 + 8 * 8) * 28
+    assert nv == (ev * 8 + 255) // 256 * 256 + ev * 128 * 4
+    assert lib.sd_paged_attention_workspace_size(32, 1, 32, 8, 128, 4096, 0) > 0
+    assert lib.sd_paged_attention_workspace_size(0, 1, 32, 8, 128, 4096, 0) == 0
     assert lib.sd_w8a16_workspace_size(1, 151936, 1024, 0) == 0  # lm_head: no split-K
     assert lib.sd_w8a16_workspace_size(1, 1024, 3072, 0) > 0      # down: split-K partials
 
