@@ -95,6 +95,13 @@ __device__ __forceinline__ int seq_keys(const AttnParams& p, int b) {
   return min(max(L, 0), p.max_ctx);
 }
 
+// seq_keys for a wave-uniform b (scalar loads).
+__device__ __forceinline__ int seq_keys_uniform(const AttnParams& p, int b) {
+  const int L = p.ctx ? sd::load_scalar_i32(p.ctx + b)
+                      : sd::load_scalar_i32(p.cu_k + b + 1) - sd::load_scalar_i32(p.cu_k + b);
+  return min(max(L, 0), p.max_ctx);
+}
+
 __device__ __forceinline__ int steps_of(int L) { return (L + kTile - 1) / kTile; }
 
 __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b) {
@@ -153,6 +160,8 @@ __device__ void locate(const AttnParams& p, int s, int& b_out, int& first_out) {
 }
 
 // Element offset of key position `tok` (0 <= tok < L) of one sequence.
+// UNIFORM: `btrow` and `tok` are the same on every lane (scalar table load).
+template <bool UNIFORM = false>
 __device__ __forceinline__ int64_t kv_row(const AttnParams& p, const int32_t* btrow, int tok) {
   int pg, off;
   if (p.bs_shift >= 0) {
@@ -162,7 +171,7 @@ __device__ __forceinline__ int64_t kv_row(const AttnParams& p, const int32_t* bt
     pg = tok / p.block_size;
     off = tok - pg * p.block_size;
   }
-  int blk = btrow[pg];
+  int blk = UNIFORM ? sd::load_scalar_i32(btrow + pg) : btrow[pg];
   blk = min(max(blk, 0), p.num_blocks - 1);  // padding ids (-1) never reach here; clamp anyway
   return static_cast<int64_t>(blk) * p.c_sblk + static_cast<int64_t>(off) * p.c_spos;
 }
@@ -252,15 +261,22 @@ void paged_attn_main(AttnParams p) {
     }
   };
 
+  // Always issues the same 16 loads (addresses clamped into the sequence; a
+  // wave without keys in the step reloads row L - 1 and ignores it): a load
+  // count that never depends on control flow lets the compiler wait for this
+  // step's loads only, not for the prefetch issued after them.
   auto load_step = [&](StepRegs& R, int lb, int lh, int lj, int L) {
-    const int t0 = lj * kTile + wave * kStep;
-    if (t0 >= L) return;  // wave-uniform: this wave has no keys in the step
     const int last = L - 1;
+    // wave-uniform by construction; readfirstlane lets the compiler prove it, so
+    // the block-table lookup is a scalar load (lgkmcnt) and never waits on the
+    // vector loads in flight
+    const int t0 = __builtin_amdgcn_readfirstlane(min(lj * kTile + wave * kStep, last));
+    lb = __builtin_amdgcn_readfirstlane(lb);
     const int32_t* btrow = p.bt + static_cast<int64_t>(lb) * p.bt_stride;
     const int64_t hoff = static_cast<int64_t>(lh) * p.c_shead;
     if constexpr (ONE_PAGE) {
       // scalar page base + 32-bit lane offsets (key rows of one page)
-      const int64_t base = kv_row(p, btrow, t0) + hoff;
+      const int64_t base = kv_row<true>(p, btrow, t0) + hoff;
       const char* kpg = reinterpret_cast<const char*>(p.kc + base);
       const char* vpg = reinterpret_cast<const char*>(p.vc + base);
 #pragma unroll
@@ -462,12 +478,14 @@ void paged_attn_main(AttnParams p) {
           nh = 0;
           do {
             ++nb;
-            nL = seq_keys(p, nb);
+            nL = seq_keys_uniform(p, nb);
           } while (nL == 0);  // sequences without keys own no steps; s + 1 < total ends the scan
         }
       }
-      load_step(nxt, nb, nh, nj, nL);
     }
+    // the last step prefetches itself again (cache-resident) so that every
+    // iteration issues the same loads
+    load_step(nxt, more ? nb : b, more ? nh : h, more ? nj : j, more ? nL : si.L);
     compute_step(cur, j);
     const bool pair_end = j + 1 == n;
     if (pair_end || !more) flush(pair_end && j_first == 0);

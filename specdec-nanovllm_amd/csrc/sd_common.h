@@ -65,6 +65,16 @@ __device__ __forceinline__ void split_pack(float a, float b, uint32_t& hi, uint3
 __device__ __forceinline__ u32x4 load16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
+// Scalar (SMEM) load of a wave-uniform address that nothing writes while the
+// kernel runs (block tables, lengths). It completes on lgkmcnt, so using the
+// value never waits for the vector loads in flight — which a vector load of the
+// same address would (vmcnt counts in order).
+__device__ __forceinline__ int32_t load_scalar_i32(const int32_t* p) {
+  int32_t v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+  return v;
+}
+
 // 16-byte load of data read once (KV cache, weights): the nontemporal hint
 // keeps the stream from displacing reusable lines in the caches.
 __device__ __forceinline__ u32x4 load16_stream(const void* p) {

@@ -16,9 +16,11 @@
 // Tiling: the weight is the MFMA A operand (16 rows n x 32 k), the activation
 // the B operand (32 k x 16 rows m; M < 16 leaves lanes zero), so each lane
 // streams 16 contiguous int8 of one weight row per 64-k step — one 16-byte
-// load, 1 KB per wave instruction. A workgroup = 4 wave64s sharing NT 16-row
-// tiles and splitting K four ways; `sgrid` workgroups split K further for
-// narrow layers (N = 1024) and a reduce kernel sums their fp32 partials.
+// nontemporal load, 1 KB per wave instruction. One launch per call: a grid of
+// resident workgroups walks the row groups (16 NT rows) grid-stride; a row
+// group is either one wave's (whole K, when rows are plentiful) or shared by
+// the four waves of a workgroup that split K and add their partials in LDS
+// (narrow layers such as N = 1024).
 //
 // int8 -> fp16: (b ^ 0x80) in the low byte under exponent byte 0x64 is the
 // fp16 value 1024 + b + 128, exact; subtracting 1152 (packed fp16) gives b.
@@ -46,9 +48,8 @@ struct W8Params {
   uint16_t* y;
   int64_t ys;
   int32_t M, N, K;
-  int32_t nks;    // K / 64
-  int32_t sgrid;  // workgroups along K
-  float* part;    // [sgrid][M][N] fp32 partial sums when sgrid > 1
+  int32_t nks;     // K / 64
+  int32_t groups;  // row groups of 16 NT rows
 };
 
 __device__ __forceinline__ float load_scale(const void* s, int dtype, int64_t i) {
@@ -92,28 +93,67 @@ template <> __device__ __forceinline__ u32x4 dequant8<__bf16>(uint32_t w0, uint3
   return r;
 }
 
-template <typename T, int MT, int NT, bool PER_GROUP>
+// Row groups of 16 NT rows are spread over the grid (grid-stride). KW waves
+// share one row group and split its K (partials meet in LDS); with KW == 1 the
+// four waves of a workgroup own four different row groups. Each wave walks its
+// (row group, K chunk) items in order and keeps the next D - 1 items' loads
+// in flight while it computes item i (a ring of D register buffers), so a
+// workgroup streams weights for its whole lifetime instead of loading once
+// and exiting.
+//
+// Weight loads are row-contiguous: a chunk is U 64-k steps (64 U bytes) of
+// each of the 16 NT rows, and 4 U lanes read one row's 64 U bytes, so a load
+// instruction covers 16 / U whole row segments. The chunk is staged in a
+// wave-private LDS tile, 16-byte unit u of row r at position u ^ (r & SWZ)
+// (SWZ = min(4 U, 16) - 1), from which each lane reads its MFMA A operand
+// (16 int8 of row l % 16 at k = 64 step + 16 (l / 16)) with ds_read_b128; with
+// 16 positions per row the 16 lanes of a read hit distinct banks.
+template <typename T, int MT, int NT, int KW, int U, bool PER_GROUP, bool CONTIG = false,
+          int D = 2>
 __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
-  constexpr int U = MT == 1 ? 4 : (MT == 2 ? 2 : 1);  // 64-k steps loaded per batch
-  __shared__ __attribute__((aligned(16))) float red[kWaves - 1][NT * MT * 4][64];
+  static_assert(U == 2 || U == 4 || U == 8, "a chunk row segment is 64 U bytes");
+  constexpr int LPR = 4 * U;         // lanes per row segment (16-byte units per row)
+  constexpr int RPI = 64 / LPR;      // row segments per load instruction
+  constexpr int NLD = 16 * NT / RPI; // load instructions per chunk
+  constexpr int NSUB = kWaves / KW;  // row groups a workgroup works on at once
+  constexpr int SWZ = (LPR < 16 ? LPR : 16) - 1;  // position swizzle stays inside a row
+  constexpr int TILE = 16 * NT * LPR * 16;  // bytes of one wave's LDS tile
+  __shared__ __attribute__((aligned(16))) char wtile[kWaves][TILE];
+  __shared__ __attribute__((aligned(16))) float red[KW > 1 ? KW - 1 : 1][NT * MT * 4][64];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
-  const int n0 = blockIdx.x * NT * 16;
-  const int sg = blockIdx.y;
-  const int m0 = blockIdx.z * MT * 16;
+  const int sub = wave / KW, kw = wave - sub * KW;
+  const int m0 = blockIdx.y * MT * 16;
+  char* tile = wtile[wave];
 
-  const int parts = kWaves * p.sgrid;
-  const int part = sg * kWaves + wave;
-  const int ks = static_cast<int>(static_cast<int64_t>(part) * p.nks / parts);
-  const int ke = static_cast<int>(static_cast<int64_t>(part + 1) * p.nks / parts);
+  // K steps of this wave: [ks, ke); every wave of a row group runs the same
+  // number of chunks (so the LDS reduction lines up), short ones skip steps.
+  const int ks = static_cast<int>(static_cast<int64_t>(kw) * p.nks / KW);
+  const int ke = static_cast<int>(static_cast<int64_t>(kw + 1) * p.nks / KW);
+  const int nchunks = ((p.nks + KW - 1) / KW + U - 1) / U;
 
-  const int8_t* wp[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int n = min(n0 + nt * 16 + lr, p.N - 1);  // rows past N: read a valid row, drop result
-    wp[nt] = p.w + static_cast<int64_t>(n) * p.ws + lg * 16;
+  // row groups of this wave: g0, g0 + gstride, ... (ngroups of them). Grid-stride
+  // over the whole matrix, or (CONTIG) a contiguous range per workgroup whose
+  // NSUB waves take alternate groups, so a workgroup reads adjacent rows.
+  int g0, gstride, ngroups;
+  if constexpr (CONTIG) {
+    const int per = (p.groups + gridDim.x * NSUB - 1) / (gridDim.x * NSUB) * NSUB;
+    const int gb = blockIdx.x * per, ge = min(gb + per, p.groups);
+    g0 = gb + sub;
+    gstride = NSUB;
+    ngroups = g0 < ge ? (ge - g0 + NSUB - 1) / NSUB : 0;
+  } else {
+    g0 = blockIdx.x * NSUB + sub;
+    gstride = gridDim.x * NSUB;
+    ngroups = g0 < p.groups ? (p.groups - g0 + gstride - 1) / gstride : 0;
   }
+  const int nit = ngroups * nchunks;
+  if (nit == 0) return;  // uniform over the workgroup when KW > 1 (NSUB == 1)
+
+  // Activation rows past M are never loaded: those lanes keep zeros (only the
+  // lanes of real rows touch memory, e.g. 4 of 64 at M = 1).
   const uint16_t* xp[MT];
   bool xok[MT];
 #pragma unroll
@@ -129,40 +169,75 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto steps = [&](auto nstep, int kk) {
-    constexpr int S = decltype(nstep)::value;
-    u32x4 wv[S][NT];
-    u32x4 xv[S][MT][2];
+  // this lane's place in a load instruction: row segment, 16-byte unit
+  const int ld_row = lane / LPR, ld_unit = lane % LPR;
+  const int ld_step = ld_unit >> 2;  // 64-k step (within the chunk) of that unit
+
+  struct Regs {
+    u32x4 w[NLD];
+    u32x4 x[U][MT][2];  // activation B operands of the chunk's steps
+  };
+  // Every call issues the same loads: steps past this wave's K range are
+  // clamped into the matrix (loaded, never used), rows past N / M read a valid
+  // row whose result is dropped. A load count that never depends on control
+  // flow lets the compiler wait for one chunk without waiting for the chunks
+  // prefetched after it.
+  auto load = [&](Regs& R, int g, int c) {
+    const int n0 = g * NT * 16;
+    const int s0 = ks + c * U;
+    const int64_t kw_off = static_cast<int64_t>(min(s0 + ld_step, p.nks - 1)) * 64 +
+                           (ld_unit & 3) * 16;
 #pragma unroll
-    for (int u = 0; u < S; ++u) {
-      const int64_t k0 = static_cast<int64_t>(kk + u) * 64;
+    for (int i = 0; i < NLD; ++i) {
+      const int n = min(n0 + i * RPI + ld_row, p.N - 1);
+      R.w[i] = sd::load16_stream(p.w + static_cast<int64_t>(n) * p.ws + kw_off);
+    }
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) wv[u][nt] = sd::load16(wp[nt] + k0);
+    for (int u = 0; u < U; ++u) {
+      const int64_t k0 = static_cast<int64_t>(min(s0 + u, p.nks - 1)) * 64;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         if (xok[mt]) {
-          xv[u][mt][0] = sd::load16(xp[mt] + k0);
-          xv[u][mt][1] = sd::load16(xp[mt] + k0 + 8);
+          R.x[u][mt][0] = sd::load16(xp[mt] + k0);
+          R.x[u][mt][1] = sd::load16(xp[mt] + k0 + 8);
         } else {
-          xv[u][mt][0] = u32x4{0u, 0u, 0u, 0u};
-          xv[u][mt][1] = u32x4{0u, 0u, 0u, 0u};
+          R.x[u][mt][0] = u32x4{0u, 0u, 0u, 0u};
+          R.x[u][mt][1] = u32x4{0u, 0u, 0u, 0u};
         }
       }
     }
+  };
+
+  auto compute = [&](Regs& R, int g, int c) {
+    const int n0 = g * NT * 16;
+    const int s0 = ks + c * U;
+    // stage: row r = i * RPI + ld_row, unit ld_unit at position ld_unit ^ (r & 15)
 #pragma unroll
-    for (int u = 0; u < S; ++u) {
+    for (int i = 0; i < NLD; ++i) {
+      const int r = i * RPI + ld_row;
+      sd::store16(tile + (r * LPR + (ld_unit ^ (r & SWZ))) * 16, R.w[i]);
+    }
+    sd::wave_lds_sync();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int step = s0 + u;
+      if (step >= ke) break;  // wave-uniform
+      const int64_t k0 = static_cast<int64_t>(step) * 64;
+      const u32x4(&xv)[MT][2] = R.x[u];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const u32x4 a0 = dequant8<T>(wv[u][nt].x, wv[u][nt].y);  // k = 16 lg + 0..7
-        const u32x4 a1 = dequant8<T>(wv[u][nt].z, wv[u][nt].w);  // k = 16 lg + 8..15
+        const int r = nt * 16 + lr;
+        const u32x4 wv = sd::load16(tile + (r * LPR + ((u * 4 + lg) ^ (r & SWZ))) * 16);
+        const u32x4 a0 = dequant8<T>(wv.x, wv.y);  // k = 16 lg + 0..7
+        const u32x4 a1 = dequant8<T>(wv.z, wv.w);  // k = 16 lg + 8..15
         if constexpr (!PER_GROUP) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            acc[nt][mt] = sd::Elem<T>::mfma(a0, xv[u][mt][0], acc[nt][mt]);
-            acc[nt][mt] = sd::Elem<T>::mfma(a1, xv[u][mt][1], acc[nt][mt]);
+            acc[nt][mt] = sd::Elem<T>::mfma(a0, xv[mt][0], acc[nt][mt]);
+            acc[nt][mt] = sd::Elem<T>::mfma(a1, xv[mt][1], acc[nt][mt]);
           }
         } else {
-          const int grp = static_cast<int>((static_cast<int64_t>(kk + u) * 64) / p.group);
+          const int grp = static_cast<int>(k0 / p.group);
           const int ng = p.K / p.group;
           float sc[4];
 #pragma unroll
@@ -173,154 +248,206 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             f32x4 t = {0.f, 0.f, 0.f, 0.f};
-            t = sd::Elem<T>::mfma(a0, xv[u][mt][0], t);
-            t = sd::Elem<T>::mfma(a1, xv[u][mt][1], t);
+            t = sd::Elem<T>::mfma(a0, xv[mt][0], t);
+            t = sd::Elem<T>::mfma(a1, xv[mt][1], t);
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[nt][mt][i] += t[i] * sc[i];
           }
         }
       }
     }
+    sd::wave_lds_sync();  // every lane has read the tile before the next chunk overwrites it
   };
 
-  int kk = ks;
-  for (; kk + U <= ke; kk += U) steps(std::integral_constant<int, U>{}, kk);
-  for (; kk < ke; ++kk) steps(std::integral_constant<int, 1>{}, kk);
-
-  // ---- reduce the four K slices of this workgroup
-  if (wave > 0) {
+  // lane holds y^T[n = n0 + 16 nt + 4 lg + i][m = m0 + 16 mt + lr]
+  auto epilogue = [&](int g) {
+    if constexpr (KW > 1) {
+      if (kw > 0) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[kw - 1][(nt * MT + mt) * 4 + i][lane] = acc[nt][mt][i];
+      }
+      __syncthreads();
+      if (kw == 0) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int w = 0; w < KW - 1; ++w) acc[nt][mt][i] += red[w][(nt * MT + mt) * 4 + i][lane];
+      }
+    }
+    if (kw == 0) {
+      const int n0 = g * NT * 16;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = m0 + mt * 16 + lr;
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int nb = n0 + nt * 16 + lg * 4;
+          if (nb >= p.N) continue;
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int n = min(nb + i, p.N - 1);
+            const float sc = PER_GROUP ? 1.f : load_scale(p.scale, p.scale_dtype, n);
+            v[i] = acc[nt][mt][i] * sc + (p.bias ? sd::from_bits<T>(p.bias[n]) : 0.f);
+          }
+          uint16_t* dst = p.y + static_cast<int64_t>(m) * p.ys + nb;
+          if (nb + 3 < p.N && (reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(sd::pack2<T>(v[0], v[1]), sd::pack2<T>(v[2], v[3]));
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (nb + i < p.N) dst[i] = sd::to_bits<T>(v[i]);
+          }
+        }
+      }
+    }
+    if constexpr (KW > 1) __syncthreads();  // `red` is free for the next row group
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave - 1][(nt * MT + mt) * 4 + i][lane] = acc[nt][mt][i];
-  }
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int w = 0; w < kWaves - 1; ++w) acc[nt][mt][i] += red[w][(nt * MT + mt) * 4 + i][lane];
+      for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
 
-  // ---- lane holds y^T[n = n0 + 16 nt + 4 lg + i][m = m0 + 16 mt + lr]
+  // ring of D register buffers: item i + D - 1 is loaded while item i computes
+  Regs ring[D];
+  auto group_of = [&](int i) { return g0 + (i / nchunks) * gstride; };
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = m0 + mt * 16 + lr;
-    if (m >= p.M) continue;
+  for (int d = 0; d < D - 1; ++d) {
+    const int i = min(d, nit - 1);
+    load(ring[d], group_of(i), i % nchunks);
+  }
+  for (int it = 0; it < nit; it += D) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int nb = n0 + nt * 16 + lg * 4;
-      if (nb >= p.N) continue;
-      if (p.sgrid > 1) {
-        float* dst = p.part + (static_cast<int64_t>(sg) * p.M + m) * p.N;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (nb + i < p.N) dst[nb + i] = acc[nt][mt][i];
-        continue;
-      }
-      float v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int n = min(nb + i, p.N - 1);
-        float s = PER_GROUP ? 1.f : load_scale(p.scale, p.scale_dtype, n);
-        v[i] = acc[nt][mt][i] * s + (p.bias ? sd::from_bits<T>(p.bias[n]) : 0.f);
-      }
-      uint16_t* dst = p.y + static_cast<int64_t>(m) * p.ys + nb;
-      if (nb + 3 < p.N && (reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(sd::pack2<T>(v[0], v[1]), sd::pack2<T>(v[2], v[3]));
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (nb + i < p.N) dst[i] = sd::to_bits<T>(v[i]);
-      }
+    for (int d = 0; d < D; ++d) {
+      const int cur = it + d;
+      if (cur >= nit) break;  // wave-uniform (workgroup-uniform when KW > 1)
+      const int ahead = min(cur + D - 1, nit - 1);  // past the end: reload the last item
+      load(ring[(d + D - 1) % D], group_of(ahead), ahead % nchunks);
+      const int gi = group_of(cur), ci = cur % nchunks;
+      compute(ring[d], gi, ci);
+      if (ci + 1 == nchunks) epilogue(gi);
     }
   }
 }
 
-// y[m, n] = T(scale[n] * sum_s part[s, m, n] + bias[n]) (scale = 1 for per group).
-template <typename T>
-__global__ __launch_bounds__(kThreads) void w8a16_reduce(W8Params p) {
-  const int64_t total = static_cast<int64_t>(p.M) * p.N;
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * kThreads) {
-    const int m = static_cast<int>(i / p.N), n = static_cast<int>(i - static_cast<int64_t>(m) * p.N);
-    float a = 0.f;
-    for (int s = 0; s < p.sgrid; ++s) a += p.part[static_cast<int64_t>(s) * total + i];
-    const float sc = p.group == 0 ? load_scale(p.scale, p.scale_dtype, n) : 1.f;
-    const float v = a * sc + (p.bias ? sd::from_bits<T>(p.bias[n]) : 0.f);
-    p.y[static_cast<int64_t>(m) * p.ys + n] = sd::to_bits<T>(v);
-  }
-}
-
 struct W8Plan {
-  int MT, NT, sgrid, mblocks;
+  int MT, NT, KW, mblocks, groups, grid;
 };
+
+// Compute units of the current device (cached per device id).
+int w8_device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0)
+    n = 256;
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
+}
 
 W8Plan make_plan(int64_t M, int64_t N, int64_t K) {
   W8Plan pl;
   pl.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   pl.mblocks = static_cast<int>((M + pl.MT * 16 - 1) / (pl.MT * 16));
   const int64_t nr = (N + 15) / 16;
-  pl.NT = nr >= 4 * 1024 ? 4 : (nr >= 2 * 1024 ? 2 : 1);
-  const int64_t wgs = (nr + pl.NT - 1) / pl.NT * pl.mblocks;
+  const int cus = w8_device_cus();
   const int64_t nks = K / 64;
-  int64_t sg = (1024 + wgs - 1) / wgs;
-  const int64_t sg_max = nks / kWaves > 0 ? nks / kWaves : 1;  // >= 1 step per wave
-  if (sg > sg_max) sg = sg_max;
-  if (sg < 1) sg = 1;
-  pl.sgrid = static_cast<int>(sg);
+  // Enough 16-row tiles for ~8 waves per CU: every wave owns whole rows, two
+  // (MT <= 2) or four tiles at a time. Otherwise four waves split K of one tile.
+  if (nr * pl.mblocks >= 8ll * cus || nks < 4) {
+    pl.KW = 1;
+    pl.NT = pl.MT == 4 ? 4 : 2;
+    if (nr < pl.NT) pl.NT = 1;
+  } else {
+    pl.KW = 4;
+    pl.NT = 1;
+  }
+  pl.groups = static_cast<int>((nr + pl.NT - 1) / pl.NT);
+  const int nsub = kWaves / pl.KW;
+  const int64_t need = (pl.groups + nsub - 1) / nsub;
+  pl.grid = static_cast<int>(need < (1 << 30) ? need : (1 << 30));  // capped at launch
   return pl;
 }
 
-template <typename T, int MT, int NT, bool PG>
-void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((w8a16_kernel<T, MT, NT, PG>), grid, dim3(kThreads), 0, st, p);
+// Resident workgroups per CU of one kernel instance (cached per device).
+template <typename Kern>
+int resident_wgs(Kern kern) {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, 0) != hipSuccess || n <= 0)
+    n = 1;
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
 }
 
-template <typename T, bool PG>
-void launch_mt(const W8Params& p, const W8Plan& pl, dim3 grid, hipStream_t st) {
-  switch (pl.MT * 8 + pl.NT) {
-    case 1 * 8 + 1: launch_k<T, 1, 1, PG>(p, grid, st); break;
-    case 1 * 8 + 2: launch_k<T, 1, 2, PG>(p, grid, st); break;
-    case 1 * 8 + 4: launch_k<T, 1, 4, PG>(p, grid, st); break;
-    case 2 * 8 + 1: launch_k<T, 2, 1, PG>(p, grid, st); break;
-    case 2 * 8 + 2: launch_k<T, 2, 2, PG>(p, grid, st); break;
-    case 2 * 8 + 4: launch_k<T, 2, 4, PG>(p, grid, st); break;
-    case 4 * 8 + 1: launch_k<T, 4, 1, PG>(p, grid, st); break;
-    case 4 * 8 + 2: launch_k<T, 4, 2, PG>(p, grid, st); break;
-    default: launch_k<T, 4, 4, PG>(p, grid, st); break;
+template <typename T, int MT, int NT, int KW, bool PG>
+void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
+  constexpr int U = NT >= 2 ? 2 : 4;  // 64-k steps per chunk
+  auto kern = w8a16_kernel<T, MT, NT, KW, U, PG>;
+  // exactly one resident set of workgroups: a partial second round would
+  // leave most of the GPU idle at the end
+  const unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs(kern));
+  if (grid.x > cap) grid.x = cap;
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, p);
+}
+
+template <typename T, bool PG, int KW>
+void launch_kw(const W8Params& p, const W8Plan& pl, dim3 grid, hipStream_t st) {
+  if constexpr (KW == 1) {
+    switch (pl.MT * 8 + pl.NT) {
+      case 1 * 8 + 1: launch_k<T, 1, 1, 1, PG>(p, grid, st); break;
+      case 1 * 8 + 2: launch_k<T, 1, 2, 1, PG>(p, grid, st); break;
+      case 2 * 8 + 1: launch_k<T, 2, 1, 1, PG>(p, grid, st); break;
+      case 2 * 8 + 2: launch_k<T, 2, 2, 1, PG>(p, grid, st); break;
+      case 4 * 8 + 1: launch_k<T, 4, 1, 1, PG>(p, grid, st); break;
+      default: launch_k<T, 4, 4, 1, PG>(p, grid, st); break;
+    }
+  } else {
+    switch (pl.MT) {
+      case 1: launch_k<T, 1, 1, KW, PG>(p, grid, st); break;
+      case 2: launch_k<T, 2, 1, KW, PG>(p, grid, st); break;
+      default: launch_k<T, 4, 1, KW, PG>(p, grid, st); break;
+    }
   }
 }
 
 template <typename T>
 int launch_all(const W8Params& p, const W8Plan& pl, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((p.N + pl.NT * 16 - 1) / (pl.NT * 16)), pl.sgrid,
-                  pl.mblocks);
-  if (p.group == 0) launch_mt<T, false>(p, pl, grid, st);
-  else launch_mt<T, true>(p, pl, grid, st);
-  int rc = sd::check_launch("w8a16 main");
-  if (rc != SD_OK || pl.sgrid <= 1) return rc;
-  const int64_t total = static_cast<int64_t>(p.M) * p.N;
-  int64_t blocks = (total + kThreads - 1) / kThreads;
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL((w8a16_reduce<T>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                     st, p);
-  return sd::check_launch("w8a16 reduce");
+  const dim3 grid(static_cast<unsigned>(pl.grid), static_cast<unsigned>(pl.mblocks));
+  if (p.group == 0) {
+    if (pl.KW == 1) launch_kw<T, false, 1>(p, pl, grid, st);
+    else launch_kw<T, false, 4>(p, pl, grid, st);
+  } else {
+    if (pl.KW == 1) launch_kw<T, true, 1>(p, pl, grid, st);
+    else launch_kw<T, true, 4>(p, pl, grid, st);
+  }
+  return sd::check_launch("w8a16");
 }
 
 }  // namespace
 
 extern "C" size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_size) {
+  (void)M;
+  (void)N;
+  (void)K;
   (void)group_size;
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  const W8Plan pl = make_plan(M, N, K);
-  if (pl.sgrid <= 1) return 0;
-  return static_cast<size_t>(pl.sgrid) * M * N * sizeof(float);
+  return 0;  // one launch; K splits are reduced inside the workgroup
 }
 
 extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w,
@@ -365,12 +492,8 @@ extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* 
     return SD_ERR_UNSUPPORTED;
   }
   const W8Plan pl = make_plan(M, N, K);
-  const size_t need = pl.sgrid > 1 ? static_cast<size_t>(pl.sgrid) * M * N * sizeof(float) : 0;
-  if (need > 0 && (!workspace || workspace_bytes < need || !sd::aligned16(workspace))) {
-    sd::set_error("w8a16: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
-                  workspace ? workspace_bytes : (size_t)0);
-    return SD_ERR_WORKSPACE;
-  }
+  (void)workspace;
+  (void)workspace_bytes;
   W8Params p;
   p.x = static_cast<const uint16_t*>(x);
   p.xs = x_stride_m;
@@ -386,8 +509,7 @@ extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* 
   p.N = static_cast<int32_t>(N);
   p.K = static_cast<int32_t>(K);
   p.nks = static_cast<int32_t>(K / 64);
-  p.sgrid = pl.sgrid;
-  p.part = need > 0 ? static_cast<float*>(workspace) : nullptr;
+  p.groups = pl.groups;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == SD_BF16) return launch_all<__bf16>(p, pl, st);
   return launch_all<_Float16>(p, pl, st);
