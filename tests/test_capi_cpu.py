@@ -105,8 +105,9 @@ def test_workspace_queries():
     assert nv == (ev * 8 + 255) // 256 * 256 + ev * 128 * 4
     assert lib.sd_paged_attention_workspace_size(32, 1, 32, 8, 128, 4096, 0) > 0
     assert lib.sd_paged_attention_workspace_size(0, 1, 32, 8, 128, 4096, 0) == 0
-    assert lib.sd_w8a16_workspace_size(1, 151936, 1024, 0) == 0  # lm_head: no split-K
-    assert lib.sd_w8a16_workspace_size(1, 1024, 3072, 0) > 0      # down: split-K partials
+    # W8A16 is one launch for every shape (K splits are added inside a workgroup)
+    for M, N, K in [(1, 151936, 1024), (1, 1024, 3072), (56, 4096, 1024)]:
+        assert lib.sd_w8a16_workspace_size(M, N, K, 0) == 0
 
 
 def test_ops_refuse_cpu_tensors():
