@@ -142,7 +142,10 @@ int sd_paged_attention_partial(const void* q, int64_t q_stride_tok, int64_t q_st
                                int32_t num_splits, void* stream);
 
 /*
- * Bytes of fp32 split-K workspace that sd_w8a16_linear needs for this shape.
+ * Bytes of workspace that sd_w8a16_linear needs for this shape. Always 0 in
+ * this implementation (one launch; K splits are reduced inside a workgroup);
+ * the query and the workspace arguments stay in the ABI so callers need not
+ * change if a shape ever needs scratch memory.
  */
 size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_size);
 
@@ -158,7 +161,7 @@ size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_si
  *   y     : (M, N) dtype, row stride y_stride_m
  * Dequantization is fused (int8 -> fp in registers, fp32 accumulation, scale
  * applied to the fp32 accumulator). Supported: K % 64 == 0, group_size 0 or a
- * multiple of 64 dividing K.
+ * multiple of 64 dividing K. `workspace` may be NULL.
  */
 int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t w_stride_n,
                     const void* scale, int32_t scale_dtype, int32_t group_size,

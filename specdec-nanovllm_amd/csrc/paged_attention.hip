@@ -261,11 +261,12 @@ void paged_attn_main(AttnParams p) {
     }
   };
 
-  // Always issues the same 16 loads (addresses clamped into the sequence; a
-  // wave without keys in the step reloads row L - 1 and ignores it): a load
-  // count that never depends on control flow lets the compiler wait for this
-  // step's loads only, not for the prefetch issued after them.
-  auto load_step = [&](StepRegs& R, int lb, int lh, int lj, int L) {
+  // Always issues the same 16 loads: a load count that never depends on control
+  // flow lets the compiler wait for this step's loads only, not for the
+  // prefetch issued after them. Loads nobody uses (`real` false, or a wave
+  // without keys in the step) all read one 16-byte location, so they cost one
+  // cache line, not a re-read of streamed (nontemporal) rows.
+  auto load_step = [&](StepRegs& R, int lb, int lh, int lj, int L, bool real) {
     const int last = L - 1;
     // wave-uniform by construction; readfirstlane lets the compiler prove it, so
     // the block-table lookup is a scalar load (lgkmcnt) and never waits on the
@@ -274,6 +275,7 @@ void paged_attn_main(AttnParams p) {
     lb = __builtin_amdgcn_readfirstlane(lb);
     const int32_t* btrow = p.bt + static_cast<int64_t>(lb) * p.bt_stride;
     const int64_t hoff = static_cast<int64_t>(lh) * p.c_shead;
+    const bool used = real && lj * kTile + wave * kStep <= last;  // wave-uniform
     if constexpr (ONE_PAGE) {
       // scalar page base + 32-bit lane offsets (key rows of one page)
       const int64_t base = kv_row<true>(p, btrow, t0) + hoff;
@@ -282,14 +284,15 @@ void paged_attn_main(AttnParams p) {
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         const uint32_t off =  // bytes
-            (static_cast<uint32_t>(min(t0 + r * 4 + lg, last) - t0) * p.c_spos32 + lr * 8) * 2u;
+            used ? (static_cast<uint32_t>(min(t0 + r * 4 + lg, last) - t0) * p.c_spos32 + lr * 8) * 2u
+                 : 0u;
         R.k[r] = sd::load16_stream(kpg + off);
         R.v[r] = sd::load16_stream(vpg + off);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        const int64_t off = kv_row(p, btrow, min(t0 + r * 4 + lg, last)) + hoff + lr * 8;
+        const int64_t off = used ? kv_row(p, btrow, min(t0 + r * 4 + lg, last)) + hoff + lr * 8 : 0;
         R.k[r] = sd::load16_stream(p.kc + off);
         R.v[r] = sd::load16_stream(p.vc + off);
       }
@@ -464,7 +467,7 @@ void paged_attn_main(AttnParams p) {
   // ---- walk [s0, s1): load step s + 1 while computing step s
   begin_pair();
   StepRegs ra, rb;
-  load_step(ra, b, h, j, si.L);
+  load_step(ra, b, h, j, si.L, true);
   int s = s0;
   auto advance = [&](StepRegs& cur, StepRegs& nxt) -> bool {
     // position of step s + 1
@@ -483,9 +486,9 @@ void paged_attn_main(AttnParams p) {
         }
       }
     }
-    // the last step prefetches itself again (cache-resident) so that every
-    // iteration issues the same loads
-    load_step(nxt, more ? nb : b, more ? nh : h, more ? nj : j, more ? nL : si.L);
+    // the last step issues a dummy prefetch so that every iteration issues the
+    // same loads
+    load_step(nxt, more ? nb : b, more ? nh : h, more ? nj : j, more ? nL : si.L, more);
     compute_step(cur, j);
     const bool pair_end = j + 1 == n;
     if (pair_end || !more) flush(pair_end && j_first == 0);

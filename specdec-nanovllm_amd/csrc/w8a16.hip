@@ -182,7 +182,9 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
   // row whose result is dropped. A load count that never depends on control
   // flow lets the compiler wait for one chunk without waiting for the chunks
   // prefetched after it.
-  auto load = [&](Regs& R, int g, int c) {
+  // `real` false (prefetch past the last item): every lane reads the same 16
+  // bytes, one cache line instead of a re-read of streamed weight rows.
+  auto load = [&](Regs& R, int g, int c, bool real) {
     const int n0 = g * NT * 16;
     const int s0 = ks + c * U;
     const int64_t kw_off = static_cast<int64_t>(min(s0 + ld_step, p.nks - 1)) * 64 +
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int n = min(n0 + i * RPI + ld_row, p.N - 1);
-      R.w[i] = sd::load16_stream(p.w + static_cast<int64_t>(n) * p.ws + kw_off);
+      R.w[i] = sd::load16_stream(real ? p.w + static_cast<int64_t>(n) * p.ws + kw_off : p.w);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -324,15 +326,15 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 #pragma unroll
   for (int d = 0; d < D - 1; ++d) {
     const int i = min(d, nit - 1);
-    load(ring[d], group_of(i), i % nchunks);
+    load(ring[d], group_of(i), i % nchunks, d < nit);
   }
   for (int it = 0; it < nit; it += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int cur = it + d;
       if (cur >= nit) break;  // wave-uniform (workgroup-uniform when KW > 1)
-      const int ahead = min(cur + D - 1, nit - 1);  // past the end: reload the last item
-      load(ring[(d + D - 1) % D], group_of(ahead), ahead % nchunks);
+      const int ahead = min(cur + D - 1, nit - 1);  // past the end: dummy loads
+      load(ring[(d + D - 1) % D], group_of(ahead), ahead % nchunks, cur + D - 1 < nit);
       const int gi = group_of(cur), ci = cur % nchunks;
       compute(ring[d], gi, ci);
       if (ci + 1 == nchunks) epilogue(gi);
