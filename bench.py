@@ -13,7 +13,8 @@ Also reported on the same JSON line:
                 algorithmic bytes per launch / its average duration, measured
                 with HIP events around each launch on the launching stream
   cpu_baseline  the numpy oracle (fp32) on host cores over a bounded sample
-  extra         C3 verify, C4 W8A16 (all shapes x M, cold weights) and the
+  extra         C3 verify, C4 W8A16 (all shapes x M, cold weights), C5 draft
+                chain (us per draft step, attention / GEMV shares) and the
                 attention op split into main + combine
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -198,6 +199,31 @@ def bench_w8a16(ops, workloads, torch, steps):
     return rows
 
 
+def bench_draft_chain(workloads_mod, torch, reps=5):
+    """C5: hipGraph-captured k = 6 greedy draft steps of a random-init
+    Qwen3-0.6B (28 layers, all linears W8A16, paged bf16 KV with a 2048-token
+    context) at B in {1, 16}: us per draft step, algorithmic GB/s, and the
+    shares of attention (store + paged attention) and of the W8A16 GEMVs, each
+    timed as its own graph over the same shapes."""
+    from specdec_nanovllm_amd.draft_chain import DraftChain
+    rows = []
+    for B in (1, 16):
+        ch = DraftChain(B, ctx_len=2048, k=6, seed=B)
+        out = {"config": f"C5 draft chain B={B} ctx 2048 k=6"}
+        for name, fn in (("step", ch.chain), ("attention", ch.attention_chain),
+                         ("gemv", ch.gemv_chain)):
+            g = graph_of(fn, torch)
+            out[f"{name}_us"] = round(time_replays([g], reps, 1, torch) * 1e3 / ch.k, 2)
+        out["GBps"] = round(ch.step_bytes() / out["step_us"] / 1e3, 1)
+        out["attention_share"] = round(out["attention_us"] / out["step_us"], 3)
+        out["gemv_share"] = round(out["gemv_us"] / out["step_us"], 3)
+        out["bytes_per_step"] = ch.step_bytes()
+        rows.append(out)
+        del ch, g
+        torch.cuda.empty_cache()
+    return rows
+
+
 # ---------------------------------------------------------------------------- profile
 def profile_pass(ops, workloads, torch):
     """A few launches of each kernel plus a 512 MiB device copy (known bytes) so
@@ -325,6 +351,8 @@ def main():
         extra["verify"] = bench_verify(ops, workloads, torch, args.steps)
         torch.cuda.empty_cache()
         extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100))
+        torch.cuda.empty_cache()
+        extra["draft_chain"] = bench_draft_chain(workloads, torch)
         line["extra"] = extra
     print(json.dumps(line), flush=True)
 

@@ -1,0 +1,206 @@
+"""C5 workload: the draft model's k-step decode chain on this library's kernels.
+
+A random-init Qwen3-0.6B-shaped decoder stack (28 layers, hidden 1024, 16 q /
+8 kv heads of 128, intermediate 3072, vocab 151936, RMSNorm eps 1e-6, per-head
+q/k RMSNorm, rotate-half RoPE with theta 1e6 — nanovllm/models/qwen3.py:14-216,
+layers/layernorm.py, layers/rotary_embedding.py). Every linear (qkv, o, gate_up,
+down and lm_head) is W8A16 per-channel int8, quantized once at construction
+with ``layers.quant.quantize_weight``; the KV cache is bf16, paged in 256-token
+blocks, filled with a synthetic (random) ``ctx_len``-token context per sequence.
+
+One draft step is the reference's batched single-token forward
+(nanovllm/spec_decode/draft_proposer.py:493-510, :527-550): per sequence the
+position is ``ctx_len + s``, the slot ``bt[pos // 256] * 256 + pos % 256`` and
+the key count ``pos + 1``; the layers call ``store_kvcache``, paged decode
+attention and the W8A16 linears of this library, and the next token is the
+argmax of the logits (the greedy draft). The hot-path ops run on the gfx950
+kernels; RMSNorm, RoPE, SiLU*mul, the embedding lookup and the argmax are plain
+eager torch (no torch.compile), as the neighbours of the path.
+
+``chain()`` runs ``k`` steps back to back, each feeding its tokens to the next,
+on static buffers, so the whole chain can be captured in one HIP graph.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import ops
+from .layers.quant import quantize_weight
+
+QWEN3_06B = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, inter=3072,
+                 vocab=151936, theta=1e6, eps=1e-6)
+
+
+class DraftChain:
+    """Static-buffer k-step greedy draft decode for ``batch`` sequences."""
+
+    def __init__(self, batch: int, *, ctx_len: int = 2048, k: int = 6, layers: int = 28,
+                 hidden: int = 1024, heads: int = 16, kv_heads: int = 8, head_dim: int = 128,
+                 inter: int = 3072, vocab: int = 151936, theta: float = 1e6, eps: float = 1e-6,
+                 block_size: int = 256, seed: int = 0, device="cuda",
+                 dtype: torch.dtype = torch.bfloat16):
+        self.B, self.ctx_len, self.k = batch, ctx_len, k
+        self.L, self.H, self.Hq, self.Hkv, self.D = layers, hidden, heads, kv_heads, head_dim
+        self.I, self.V, self.eps, self.bs = inter, vocab, eps, block_size
+        self.dev, self.dtype = torch.device(device), dtype
+        self.scale = head_dim ** -0.5
+        g = torch.Generator(device=self.dev)
+        g.manual_seed(seed)
+
+        def randn(*shape, std=0.02):
+            return (torch.randn(shape, generator=g, device=self.dev) * std).to(dtype)
+
+        def qlinear(n_out, n_in):
+            q, s = quantize_weight(randn(n_out, n_in))
+            return q, s
+
+        self.embed = randn(vocab, hidden)
+        self.layers = []
+        qkv_out = (heads + 2 * kv_heads) * head_dim
+        for _ in range(layers):
+            self.layers.append(dict(
+                in_norm=1.0 + randn(hidden, std=0.1), post_norm=1.0 + randn(hidden, std=0.1),
+                q_norm=1.0 + randn(head_dim, std=0.1), k_norm=1.0 + randn(head_dim, std=0.1),
+                qkv=qlinear(qkv_out, hidden), o=qlinear(hidden, heads * head_dim),
+                gate_up=qlinear(2 * inter, hidden), down=qlinear(hidden, inter)))
+        self.final_norm = 1.0 + randn(hidden, std=0.1)
+        self.lm_head = qlinear(vocab, hidden)
+
+        # RoPE cos/sin for the positions the chain touches (rotate-half layout)
+        inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32,
+                                                 device=self.dev) / head_dim))
+        pos = torch.arange(ctx_len + k + 1, dtype=torch.float32, device=self.dev)
+        freqs = pos[:, None] * inv_freq[None, :]
+        self.cos, self.sin = freqs.cos(), freqs.sin()
+
+        # paged KV cache: (2, layers, blocks, bs, Hkv, D), a synthetic prefilled
+        # context of ctx_len rows per sequence; pages are a seeded shuffle
+        self.pages_per_seq = math.ceil((ctx_len + k) / block_size)
+        nblk = batch * self.pages_per_seq
+        self.kv = torch.randn((2, layers, nblk, block_size, kv_heads, head_dim), generator=g,
+                              device=self.dev).to(dtype)
+        cg = torch.Generator().manual_seed(seed + 1)
+        perm = torch.randperm(nblk, generator=cg).to(torch.int32)
+        self.block_table = perm.view(batch, self.pages_per_seq).to(self.dev)
+
+        # per-step static metadata: positions, slots, key counts
+        bt = perm.view(batch, self.pages_per_seq)
+        p = torch.arange(k, dtype=torch.int64)[:, None] + ctx_len  # (k, 1)
+        pos_k = p.expand(k, batch)
+        blk = bt.gather(1, (pos_k // block_size).T.contiguous()).T  # (k, B)
+        self.positions = pos_k.to(self.dev)
+        self.slots = (blk.to(torch.int64) * block_size + pos_k % block_size).to(torch.int32).to(self.dev)
+        self.ctx = (pos_k + 1).to(torch.int32).to(self.dev)
+
+        # static token buffers: tokens[0] = the last context token, tokens[s+1] = step s output
+        self.tokens = torch.randint(0, vocab, (k + 1, batch), generator=cg).to(self.dev)
+
+    # ------------------------------------------------------------------ neighbours
+    def _rms(self, x, w):
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return xf.to(x.dtype) * w
+
+    def _add_rms(self, x, residual, w):
+        xf = x.float() + residual.float()
+        residual = xf.to(x.dtype)
+        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return xf.to(x.dtype) * w, residual
+
+    def _rope(self, x, cos, sin):
+        x1, x2 = x.float().chunk(2, dim=-1)
+        c, s = cos[:, None, :], sin[:, None, :]
+        return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
+
+    # ----------------------------------------------------------------------- step
+    def step(self, s: int) -> torch.Tensor:
+        """Draft step s: reads tokens[s], writes and returns tokens[s + 1]."""
+        B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
+        pos = self.positions[s]
+        cos, sin = self.cos[pos], self.sin[pos]
+        slots, ctx = self.slots[s], self.ctx[s]
+        h = self.embed[self.tokens[s]]
+        residual = None
+        for li, lw in enumerate(self.layers):
+            if residual is None:
+                residual = h
+                x = self._rms(h, lw["in_norm"])
+            else:
+                x, residual = self._add_rms(h, residual, lw["in_norm"])
+            qkv = ops.w8a16_linear(x, *lw["qkv"])
+            q, kk, v = qkv.split([Hq * D, Hkv * D, Hkv * D], dim=-1)
+            q = self._rms(q.reshape(B, Hq, D), lw["q_norm"])
+            kk = self._rms(kk.reshape(B, Hkv, D), lw["k_norm"])
+            q, kk = self._rope(q, cos, sin), self._rope(kk, cos, sin)
+            v = v.reshape(B, Hkv, D)
+            kc, vc = self.kv[0, li], self.kv[1, li]
+            ops.store_kvcache(kk, v, kc, vc, slots)
+            o = ops.paged_attention(q, kc, vc, self.block_table, self.scale, context_lens=ctx)
+            h = ops.w8a16_linear(o.reshape(B, Hq * D), *lw["o"])
+            x, residual = self._add_rms(h, residual, lw["post_norm"])
+            gu = ops.w8a16_linear(x, *lw["gate_up"])
+            gate, up = gu.chunk(2, dim=-1)
+            h = ops.w8a16_linear(torch.nn.functional.silu(gate) * up, *lw["down"])
+        x, _ = self._add_rms(h, residual, self.final_norm)
+        logits = ops.w8a16_linear(x, *self.lm_head)
+        nxt = logits.argmax(dim=-1)
+        self.tokens[s + 1].copy_(nxt)
+        return logits
+
+    def chain(self) -> None:
+        for s in range(self.k):
+            self.step(s)
+
+    # ------------------------------------------- isolated parts (time shares)
+    def attention_chain(self) -> None:
+        """Only the attention part of every layer of every step (store_kvcache +
+        paged attention), on static q / k / v of the step's shape."""
+        if not hasattr(self, "_qkv_static"):
+            g = torch.Generator(device=self.dev)
+            g.manual_seed(7)
+            self._qkv_static = (
+                torch.randn((self.B, self.Hq, self.D), generator=g, device=self.dev).to(self.dtype),
+                torch.randn((self.B, self.Hkv, self.D), generator=g, device=self.dev).to(self.dtype),
+                torch.randn((self.B, self.Hkv, self.D), generator=g, device=self.dev).to(self.dtype))
+        q, kk, v = self._qkv_static
+        for s in range(self.k):
+            for li in range(self.L):
+                kc, vc = self.kv[0, li], self.kv[1, li]
+                ops.store_kvcache(kk, v, kc, vc, self.slots[s])
+                ops.paged_attention(q, kc, vc, self.block_table, self.scale,
+                                    context_lens=self.ctx[s])
+
+    def gemv_chain(self) -> None:
+        """Only the W8A16 linears of every step (4 per layer + lm_head), on static
+        activations of the step's shape."""
+        if not hasattr(self, "_act_static"):
+            g = torch.Generator(device=self.dev)
+            g.manual_seed(8)
+            self._act_static = (
+                torch.randn((self.B, self.H), generator=g, device=self.dev).to(self.dtype),
+                torch.randn((self.B, self.Hq * self.D), generator=g, device=self.dev).to(self.dtype),
+                torch.randn((self.B, self.I), generator=g, device=self.dev).to(self.dtype))
+        xh, xo, xi = self._act_static
+        for _ in range(self.k):
+            for lw in self.layers:
+                ops.w8a16_linear(xh, *lw["qkv"])
+                ops.w8a16_linear(xo, *lw["o"])
+                ops.w8a16_linear(xh, *lw["gate_up"])
+                ops.w8a16_linear(xi, *lw["down"])
+            ops.w8a16_linear(xh, *self.lm_head)
+
+    # ----------------------------------------------------------------- accounting
+    def step_bytes(self) -> int:
+        """Algorithmic HBM bytes of one draft step: every int8 weight and scale
+        once, the visible K/V rows of every layer, the embedding rows read."""
+        w = 0
+        for lw in self.layers:
+            for name in ("qkv", "o", "gate_up", "down"):
+                q, sc = lw[name]
+                w += q.numel() + sc.numel() * sc.element_size()
+        q, sc = self.lm_head
+        w += q.numel() + sc.numel() * sc.element_size()
+        kv = self.L * self.B * (self.ctx_len + 1) * self.Hkv * self.D * 2 * 2
+        return w + kv + self.B * self.H * 2
