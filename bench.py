@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-draft-chain", action="store_true",
+                    help="skip the C5 draft-chain extra (its thousands of launches swamp a trace)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-pass", action="store_true")
     return ap.parse_args()
@@ -158,10 +160,9 @@ def bench_verify(ops, workloads, torch, steps):
     out = torch.empty_like(case["q"])
 
     def step():
-        ops.store_kvcache(case["k_new"], case["v_new"], case["k_cache"], case["v_cache"], slots)
         ops.paged_attention(case["q"], case["k_cache"], case["v_cache"], bt, case["scale"],
                             cu_seqlens_k=cuk, cu_seqlens_q=cuq, max_seqlen_q=case["k"] + 1,
-                            out=out)
+                            out=out, key=case["k_new"], value=case["v_new"], slot_mapping=slots)
     ms = time_replays([graph_of(step, torch)], steps, 10, torch)
     nbytes = (attn_bytes(case["keys"].tolist(), 32, 8, 128, 2, q_rows=case["k"] + 1)
               + case["slots"].numel() * 8 * 128 * 2 * 2 * 2)
@@ -285,10 +286,10 @@ def main():
     out = torch.empty_like(q)
 
     def step_fn(i):
-        def f():
-            ops.store_kvcache(case["k_new"], case["v_new"], kc, vc, slots[i])
-            ops.paged_attention(q, kc, vc, tables[i], case["scale"], context_lens=lens_d, out=out)
-        return f
+        # store_kvcache of the new rows + attention: one fused launch (+ combine)
+        return lambda: ops.paged_attention(q, kc, vc, tables[i], case["scale"],
+                                           context_lens=lens_d, out=out, key=case["k_new"],
+                                           value=case["v_new"], slot_mapping=slots[i])
 
     def main_fn(i):
         return lambda: ops.paged_attention(q, kc, vc, tables[i], case["scale"],
@@ -352,7 +353,8 @@ def main():
         torch.cuda.empty_cache()
         extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100))
         torch.cuda.empty_cache()
-        extra["draft_chain"] = bench_draft_chain(workloads, torch)
+        if not args.no_draft_chain:
+            extra["draft_chain"] = bench_draft_chain(workloads, torch)
         line["extra"] = extra
     print(json.dumps(line), flush=True)
 

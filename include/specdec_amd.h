@@ -142,6 +142,37 @@ int sd_paged_attention_partial(const void* q, int64_t q_stride_tok, int64_t q_st
                                int32_t num_splits, void* stream);
 
 /*
+ * store_kvcache + paged attention in one launch: the decode / verify layer call
+ * `Attention.forward` (nanovllm/layers/attention.py:59-82: store_kvcache of the
+ * new rows, then flash_attn_with_kvcache or the paged flash_attn_varlen_func).
+ * Arguments as sd_paged_attention, plus the new rows: key/value
+ * (total_q, num_kv_heads, head_dim) and slot_mapping (total_q,), row t being
+ * query row t's key/value (decode: one per sequence; verify: the n_b rows of
+ * sequence b). Result: bit for bit the same cache as sd_store_kvcache and the
+ * same output as sd_paged_attention afterwards, PROVIDED that the new rows of
+ * sequence b are its last n_b keys in block_table order with slot -1 or the
+ * slot of that position — what prepare_decode / prepare_verify and the draft
+ * proposer produce (model_runner.py:466-482,522-548, draft_proposer.py:527-550).
+ * The attention kernel reads the new rows straight from key/value and the
+ * copies into the cache ride in the second (combine) launch, so no kernel
+ * waits for the store. num_seqs == 0 with total_q > 0 only stores.
+ */
+int sd_paged_attention_store(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+                             const void* value, int64_t value_stride_tok,
+                             int64_t value_stride_head, const int32_t* slot_mapping,
+                             const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                             void* k_cache, void* v_cache, int64_t cache_stride_block,
+                             int64_t cache_stride_pos, int64_t cache_stride_head,
+                             int64_t num_blocks, int32_t block_size, const int32_t* block_table,
+                             int64_t bt_stride, int32_t max_blocks_per_seq,
+                             const int32_t* context_lens, const int32_t* cu_seqlens_k,
+                             const int32_t* cu_seqlens_q, int32_t max_qlen, int64_t total_q,
+                             int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim, float scale, int32_t dtype, void* out,
+                             int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+                             size_t workspace_bytes, int32_t num_splits, void* stream);
+
+/*
  * Bytes of workspace that sd_w8a16_linear needs for this shape. Always 0 in
  * this implementation (one launch; K splits are reduced inside a workgroup);
  * the query and the workspace arguments stay in the ABI so callers need not

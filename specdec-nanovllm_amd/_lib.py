@@ -57,6 +57,11 @@ SIGNATURES = {
         _p, _sz, _p]),                  # workspace, bytes, stream
 }
 SIGNATURES["sd_paged_attention_partial"] = SIGNATURES["sd_paged_attention"]
+SIGNATURES["sd_paged_attention_store"] = (ctypes.c_int, [
+    _p, _i64, _i64,                 # key (new rows), strides (tok, head)
+    _p, _i64, _i64,                 # value, strides
+    _p,                             # slot_mapping
+    *SIGNATURES["sd_paged_attention"][1]])
 
 _lib = None
 

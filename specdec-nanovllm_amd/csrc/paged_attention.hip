@@ -81,6 +81,13 @@ struct AttnParams {
   int32_t nwg;        // workgroups the steps are divided among
   int32_t min_steps;  // lower bound of steps per workgroup
   int32_t rmax;       // G * max_qlen
+  // Fused store_kvcache (knew == NULL: none). Query row t's key/value row is
+  // knew/vnew row t; sequence b's rows are its last n_b keys.
+  const uint16_t* knew;
+  const uint16_t* vnew;
+  int64_t kn_stok, kn_shead, vn_stok, vn_shead;
+  const int32_t* slot;  // (total_q,) cache slot of each new row, -1 = not written
+  int64_t num_slots;    // num_blocks * block_size
 };
 
 struct SeqInfo {
@@ -103,6 +110,18 @@ __device__ __forceinline__ int seq_keys_uniform(const AttnParams& p, int b) {
 }
 
 __device__ __forceinline__ int steps_of(int L) { return (L + kTile - 1) / kTile; }
+
+// First query row and row count of a wave-uniform sequence b (scalar loads).
+__device__ __forceinline__ void seq_rows_uniform(const AttnParams& p, int b, int64_t& q0, int& nq) {
+  if (p.cu_q) {
+    const int a = sd::load_scalar_i32(p.cu_q + b), e = sd::load_scalar_i32(p.cu_q + b + 1);
+    q0 = a;
+    nq = min(max(e - a, 0), p.max_qlen);
+  } else {
+    q0 = b;
+    nq = 1;
+  }
+}
 
 __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b) {
   SeqInfo s;
@@ -159,6 +178,47 @@ __device__ void locate(const AttnParams& p, int s, int& b_out, int& first_out) {
   first_out = run;
 }
 
+// Fused store: the 16-byte pieces of the new K and V rows, copied to their
+// slots bit for bit (slot -1 or outside the pool: skipped), as store_kvcache
+// does. The main kernel never reads those cache rows (it takes new rows from
+// knew / vnew), so the combine kernel, which runs after it, does the copies:
+// each thread loads its first piece on entry and writes it after its merge.
+struct StorePiece {
+  u32x4 data;
+  int64_t slot;
+  int64_t tok;
+  int head;
+  int piece;
+  bool is_v;
+};
+
+// 32-bit index math: the host caps total_q * Hkv at 2^25 for this launch.
+__device__ __forceinline__ void piece_of(const AttnParams& p, uint32_t it, StorePiece& sp) {
+  const uint32_t per = static_cast<uint32_t>(p.total_q) * p.Hkv * (kD * 2 / 16);
+  sp.is_v = it >= per;
+  uint32_t r = sp.is_v ? it - per : it;
+  sp.piece = static_cast<int>(r & 15);
+  r >>= 4;
+  const uint32_t t = r / static_cast<uint32_t>(p.Hkv);
+  sp.head = static_cast<int>(r - t * p.Hkv);
+  sp.tok = t;
+}
+
+__device__ __forceinline__ void load_piece(const AttnParams& p, StorePiece& sp) {
+  const uint16_t* src = sp.is_v ? p.vnew + sp.tok * p.vn_stok + sp.head * p.vn_shead
+                                : p.knew + sp.tok * p.kn_stok + sp.head * p.kn_shead;
+  sp.slot = p.slot[sp.tok];
+  sp.data = sd::load16(src + sp.piece * 8);
+}
+
+__device__ __forceinline__ void write_piece(const AttnParams& p, const StorePiece& sp) {
+  if (sp.slot < 0 || sp.slot >= p.num_slots) return;
+  const int64_t blk = sp.slot / p.block_size, off = sp.slot - blk * p.block_size;
+  uint16_t* dst = const_cast<uint16_t*>(sp.is_v ? p.vc : p.kc) + blk * p.c_sblk +
+                  off * p.c_spos + sp.head * p.c_shead;
+  sd::store16(dst + sp.piece * 8, sp.data);
+}
+
 // Element offset of key position `tok` (0 <= tok < L) of one sequence.
 // UNIFORM: `btrow` and `tok` are the same on every lane (scalar table load).
 template <bool UNIFORM = false>
@@ -198,6 +258,7 @@ constexpr int smem_bytes() {
 struct StepRegs {
   u32x4 k[8];
   u32x4 v[8];
+  int slotv;  // fused store, steps holding new rows: slot of new row (lane & 31)
 };
 
 // ONE_PAGE: block_size % 32 == 0, so a wave's 32-key slice never crosses a
@@ -207,7 +268,7 @@ struct StepRegs {
 template <int RT>
 constexpr int main_occupancy() { return RT == 1 ? 2 : 1; }
 
-template <typename T, int RT, bool ONE_PAGE>
+template <typename T, int RT, bool ONE_PAGE, bool STORE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(main_occupancy<RT>())))
 void paged_attn_main(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[smem_bytes<RT>()];
@@ -276,6 +337,38 @@ void paged_attn_main(AttnParams p) {
     const int32_t* btrow = p.bt + static_cast<int64_t>(lb) * p.bt_stride;
     const int64_t hoff = static_cast<int64_t>(lh) * p.c_shead;
     const bool used = real && lj * kTile + wave * kStep <= last;  // wave-uniform
+    // fused store: the sequence's last nq keys are this launch's new rows; a
+    // step that holds some reads them from knew / vnew (bits identical to what
+    // the store writes) and loads their slots beside them; compute_step swaps
+    // in the cache row for a new row whose slot is -1 (never written: the key
+    // stays the cache row, as without the store). Page lookups stay uniform;
+    // only the lanes of new rows swap their address.
+    int64_t q0 = 0;
+    int first_new = L;
+    bool fresh_step = false;
+    if constexpr (STORE) {
+      // only a step within max_qlen keys of the end can hold new rows
+      int slot_at = 0;
+      if (used && t0 + kStep > L - p.max_qlen) {
+        int nq;
+        seq_rows_uniform(p, lb, q0, nq);
+        first_new = L - nq;
+        if (nq > 0 && t0 + kStep > first_new) {
+          fresh_step = true;
+          slot_at = static_cast<int>(q0) + min(lane & 31, nq - 1);
+        }
+      }
+      // issued on every step (slot 0 when unused), like the K/V loads, so the
+      // count of loads in flight is the same on every path
+      R.slotv = p.slot[slot_at];
+    }
+    auto fresh_ptrs = [&](int tok, const void*& ks, const void*& vs) {
+      const int jn = tok - first_new;
+      if (jn >= 0) {
+        ks = p.knew + (q0 + jn) * p.kn_stok + lh * p.kn_shead + lr * 8;
+        vs = p.vnew + (q0 + jn) * p.vn_stok + lh * p.vn_shead + lr * 8;
+      }
+    };
     if constexpr (ONE_PAGE) {
       // scalar page base + 32-bit lane offsets (key rows of one page)
       const int64_t base = kv_row<true>(p, btrow, t0) + hoff;
@@ -283,18 +376,30 @@ void paged_attn_main(AttnParams p) {
       const char* vpg = reinterpret_cast<const char*>(p.vc + base);
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
+        const int tok = min(t0 + r * 4 + lg, last);
         const uint32_t off =  // bytes
-            used ? (static_cast<uint32_t>(min(t0 + r * 4 + lg, last) - t0) * p.c_spos32 + lr * 8) * 2u
-                 : 0u;
-        R.k[r] = sd::load16_stream(kpg + off);
-        R.v[r] = sd::load16_stream(vpg + off);
+            used ? (static_cast<uint32_t>(tok - t0) * p.c_spos32 + lr * 8) * 2u : 0u;
+        if (STORE && fresh_step) {
+          const void* ks = kpg + off;
+          const void* vs = vpg + off;
+          fresh_ptrs(tok, ks, vs);
+          R.k[r] = sd::load16_stream(ks);
+          R.v[r] = sd::load16_stream(vs);
+        } else {
+          R.k[r] = sd::load16_stream(kpg + off);
+          R.v[r] = sd::load16_stream(vpg + off);
+        }
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        const int64_t off = used ? kv_row(p, btrow, min(t0 + r * 4 + lg, last)) + hoff + lr * 8 : 0;
-        R.k[r] = sd::load16_stream(p.kc + off);
-        R.v[r] = sd::load16_stream(p.vc + off);
+        const int tok = min(t0 + r * 4 + lg, last);
+        const int64_t off = used ? kv_row(p, btrow, tok) + hoff + lr * 8 : 0;
+        const void* ks = p.kc + off;
+        const void* vs = p.vc + off;
+        if (STORE && fresh_step) fresh_ptrs(tok, ks, vs);
+        R.k[r] = sd::load16_stream(ks);
+        R.v[r] = sd::load16_stream(vs);
       }
     }
   };
@@ -305,6 +410,29 @@ void paged_attn_main(AttnParams p) {
   auto compute_step = [&](StepRegs& R, int cj) {
     const int tb = cj * kTile + wave * kStep;
     if (tb >= si.L) return;
+    if constexpr (STORE) {
+      // new rows of this step whose slot is not stored: their key is the cache
+      // row (rare: the engine gives -1 only to rows without keys)
+      const int first_new = si.L - si.nq;
+      if (si.nq > 0 && tb + kStep > first_new) {
+        const int sl = R.slotv;
+        const uint32_t want = si.nq >= 32 ? ~0u : (1u << si.nq) - 1u;
+        const uint32_t ok = static_cast<uint32_t>(__ballot(sl >= 0 && sl < p.num_slots)) & want;
+        if (ok != want) {
+          const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            const int tok = min(tb + r * 4 + lg, si.L - 1);
+            const int jn = tok - first_new;
+            if (jn >= 0 && !((ok >> jn) & 1u)) {
+              const int64_t row = kv_row(p, btrow, tok) + static_cast<int64_t>(h) * p.c_shead + lr * 8;
+              R.k[r] = sd::load16(p.kc + row);
+              R.v[r] = sd::load16(p.vc + row);
+            }
+          }
+        }
+      }
+    }
     // ---- stage the 32 K and V rows of this step (row-major, padded pitch)
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -519,7 +647,7 @@ void paged_attn_main(AttnParams p) {
 // workgroups that met it are f / S .. (f + n - 1) / S and workgroup w wrote
 // its partial to slot w + pair. A pair met by one workgroup is already final.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
+__device__ __forceinline__ void combine_rows(const AttnParams& p) {
   constexpr int kUnroll = 16;
   const int h = blockIdx.y, b = blockIdx.z;
   const SeqInfo si = seq_info(p, b);
@@ -580,6 +708,31 @@ __global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
   store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);
 }
 
+// STORE: the launch's share of the fused store (grid-stride over the pieces).
+template <typename T, bool STORE>
+__global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
+  if constexpr (!STORE) {
+    combine_rows<T>(p);
+  } else {
+    const uint32_t items = 2u * static_cast<uint32_t>(p.total_q) * p.Hkv * (kD * 2 / 16);
+    const uint32_t nthreads = gridDim.x * gridDim.y * gridDim.z * kThreads;
+    const uint32_t it0 =
+        ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * kThreads + threadIdx.x;
+    StorePiece sp;
+    if (it0 < items) {
+      piece_of(p, it0, sp);
+      load_piece(p, sp);
+    }
+    combine_rows<T>(p);
+    if (it0 < items) write_piece(p, sp);
+    for (uint32_t it = it0 + nthreads; it < items; it += nthreads) {
+      piece_of(p, it, sp);
+      load_piece(p, sp);
+      write_piece(p, sp);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ host
 struct Plan {
   int RT;         // 16-row tiles of query rows
@@ -632,12 +785,18 @@ size_t ws_bytes(const Plan& pl) {
   return ml_bytes(pl) + static_cast<size_t>(pl.slots) * pl.rmax * kD * sizeof(float);
 }
 
-template <typename T, int RT>
+template <typename T, int RT, bool STORE>
 void launch_main(const AttnParams& p, hipStream_t st) {
   if (p.block_size % kStep == 0)
-    hipLaunchKernelGGL((paged_attn_main<T, RT, true>), dim3(p.nwg), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((paged_attn_main<T, RT, true, STORE>), dim3(p.nwg), dim3(kThreads), 0, st, p);
   else
-    hipLaunchKernelGGL((paged_attn_main<T, RT, false>), dim3(p.nwg), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((paged_attn_main<T, RT, false, STORE>), dim3(p.nwg), dim3(kThreads), 0, st, p);
+}
+
+template <typename T, int RT>
+void launch_main(const AttnParams& p, hipStream_t st) {
+  if (p.knew) launch_main<T, RT, true>(p, st);
+  else launch_main<T, RT, false>(p, st);
 }
 
 template <typename T>
@@ -647,11 +806,23 @@ int launch_all(const AttnParams& p, const Plan& pl, bool combine, hipStream_t st
   int rc = sd::check_launch("paged_attention main");
   if (rc != SD_OK || !combine) return rc;
   const dim3 grid((pl.rmax + kThreads / 32 - 1) / (kThreads / 32), p.Hkv, p.num_seqs);
-  hipLaunchKernelGGL((paged_attn_combine<T>), grid, dim3(kThreads), 0, st, p);
+  if (p.knew)
+    hipLaunchKernelGGL((paged_attn_combine<T, true>), grid, dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((paged_attn_combine<T, false>), grid, dim3(kThreads), 0, st, p);
   return sd::check_launch("paged_attention combine");
 }
 
-int run_attention(bool combine, const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+struct NewRows {  // fused store_kvcache arguments (key == NULL: none)
+  const void* key;
+  int64_t key_stride_tok, key_stride_head;
+  const void* value;
+  int64_t value_stride_tok, value_stride_head;
+  const int32_t* slot_mapping;
+};
+
+int run_attention(bool combine, const NewRows& nr, const void* q, int64_t q_stride_tok,
+                  int64_t q_stride_head,
                   const void* k_cache, const void* v_cache, int64_t cache_stride_block,
                   int64_t cache_stride_pos, int64_t cache_stride_head, int64_t num_blocks,
                   int32_t block_size, const int32_t* block_table, int64_t bt_stride,
@@ -768,6 +939,14 @@ int run_attention(bool combine, const void* q, int64_t q_stride_tok, int64_t q_s
   p.num_seqs = num_seqs;
   p.nwg = pl.nwg;
   p.min_steps = pl.min_steps;
+  p.knew = static_cast<const uint16_t*>(nr.key);
+  p.vnew = static_cast<const uint16_t*>(nr.value);
+  p.kn_stok = nr.key_stride_tok;
+  p.kn_shead = nr.key_stride_head;
+  p.vn_stok = nr.value_stride_tok;
+  p.vn_shead = nr.value_stride_head;
+  p.slot = nr.slot_mapping;
+  p.num_slots = num_blocks * block_size;
   p.rmax = pl.rmax;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -799,7 +978,7 @@ extern "C" int sd_paged_attention(
     int32_t num_kv_heads, int32_t head_dim, float scale, int32_t dtype, void* out,
     int64_t out_stride_tok, int64_t out_stride_head, void* workspace, size_t workspace_bytes,
     int32_t num_splits, void* stream) {
-  return run_attention(true, q, q_stride_tok, q_stride_head, k_cache, v_cache,
+  return run_attention(true, NewRows{}, q, q_stride_tok, q_stride_head, k_cache, v_cache,
                        cache_stride_block, cache_stride_pos, cache_stride_head, num_blocks,
                        block_size, block_table, bt_stride, max_blocks_per_seq, context_lens,
                        cu_seqlens_k, cu_seqlens_q, max_qlen, total_q, num_seqs, num_q_heads,
@@ -817,7 +996,53 @@ extern "C" int sd_paged_attention_partial(
     int32_t num_kv_heads, int32_t head_dim, float scale, int32_t dtype, void* out,
     int64_t out_stride_tok, int64_t out_stride_head, void* workspace, size_t workspace_bytes,
     int32_t num_splits, void* stream) {
-  return run_attention(false, q, q_stride_tok, q_stride_head, k_cache, v_cache,
+  return run_attention(false, NewRows{}, q, q_stride_tok, q_stride_head, k_cache, v_cache,
+                       cache_stride_block, cache_stride_pos, cache_stride_head, num_blocks,
+                       block_size, block_table, bt_stride, max_blocks_per_seq, context_lens,
+                       cu_seqlens_k, cu_seqlens_q, max_qlen, total_q, num_seqs, num_q_heads,
+                       num_kv_heads, head_dim, scale, dtype, out, out_stride_tok,
+                       out_stride_head, workspace, workspace_bytes, num_splits, stream);
+}
+
+extern "C" int sd_paged_attention_store(
+    const void* key, int64_t key_stride_tok, int64_t key_stride_head, const void* value,
+    int64_t value_stride_tok, int64_t value_stride_head, const int32_t* slot_mapping,
+    const void* q, int64_t q_stride_tok, int64_t q_stride_head, void* k_cache, void* v_cache,
+    int64_t cache_stride_block, int64_t cache_stride_pos, int64_t cache_stride_head,
+    int64_t num_blocks, int32_t block_size, const int32_t* block_table, int64_t bt_stride,
+    int32_t max_blocks_per_seq, const int32_t* context_lens, const int32_t* cu_seqlens_k,
+    const int32_t* cu_seqlens_q, int32_t max_qlen, int64_t total_q, int32_t num_seqs,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float scale, int32_t dtype,
+    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+    size_t workspace_bytes, int32_t num_splits, void* stream) {
+  sd::clear_error();
+  if (total_q > 0 && (!key || !value || !slot_mapping)) {
+    sd::set_error("paged_attention_store: key, value and slot_mapping are required");
+    return SD_ERR_VALUE;
+  }
+  if (total_q > 0 &&
+      (!sd::aligned16(key) || !sd::aligned16(value) || key_stride_tok % 8 != 0 ||
+       key_stride_head % 8 != 0 || value_stride_tok % 8 != 0 || value_stride_head % 8 != 0)) {
+    sd::set_error("paged_attention_store: key/value rows must be 16-byte aligned");
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (total_q > 0 && num_kv_heads > 0 && total_q > (int64_t{1} << 25) / num_kv_heads) {
+    sd::set_error("paged_attention_store: total_q * num_kv_heads above 2^25");
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (num_seqs == 0 && total_q > 0) {  // rows to store but no attention: a plain store
+    if (dtype != SD_BF16 && dtype != SD_F16) {
+      sd::set_error("paged_attention_store: dtype must be bf16 or fp16");
+      return SD_ERR_VALUE;
+    }
+    return sd_store_kvcache(key, key_stride_tok, key_stride_head, value, value_stride_tok,
+                            value_stride_head, k_cache, v_cache, cache_stride_block,
+                            cache_stride_pos, cache_stride_head, slot_mapping, total_q,
+                            num_kv_heads, head_dim, block_size, num_blocks, 2, stream);
+  }
+  const NewRows nr{key, key_stride_tok, key_stride_head, value, value_stride_tok,
+                   value_stride_head, slot_mapping};
+  return run_attention(true, nr, q, q_stride_tok, q_stride_head, k_cache, v_cache,
                        cache_stride_block, cache_stride_pos, cache_stride_head, num_blocks,
                        block_size, block_table, bt_stride, max_blocks_per_seq, context_lens,
                        cu_seqlens_k, cu_seqlens_q, max_qlen, total_q, num_seqs, num_q_heads,

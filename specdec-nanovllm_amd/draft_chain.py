@@ -136,8 +136,8 @@ class DraftChain:
             q, kk = self._rope(q, cos, sin), self._rope(kk, cos, sin)
             v = v.reshape(B, Hkv, D)
             kc, vc = self.kv[0, li], self.kv[1, li]
-            ops.store_kvcache(kk, v, kc, vc, slots)
-            o = ops.paged_attention(q, kc, vc, self.block_table, self.scale, context_lens=ctx)
+            o = ops.paged_attention(q, kc, vc, self.block_table, self.scale, context_lens=ctx,
+                                    key=kk, value=v, slot_mapping=slots)  # store fused
             h = ops.w8a16_linear(o.reshape(B, Hq * D), *lw["o"])
             x, residual = self._add_rms(h, residual, lw["post_norm"])
             gu = ops.w8a16_linear(x, *lw["gate_up"])
@@ -155,8 +155,8 @@ class DraftChain:
 
     # ------------------------------------------- isolated parts (time shares)
     def attention_chain(self) -> None:
-        """Only the attention part of every layer of every step (store_kvcache +
-        paged attention), on static q / k / v of the step's shape."""
+        """Only the attention part of every layer of every step (store_kvcache
+        fused with paged attention), on static q / k / v of the step's shape."""
         if not hasattr(self, "_qkv_static"):
             g = torch.Generator(device=self.dev)
             g.manual_seed(7)
@@ -168,9 +168,9 @@ class DraftChain:
         for s in range(self.k):
             for li in range(self.L):
                 kc, vc = self.kv[0, li], self.kv[1, li]
-                ops.store_kvcache(kk, v, kc, vc, self.slots[s])
                 ops.paged_attention(q, kc, vc, self.block_table, self.scale,
-                                    context_lens=self.ctx[s])
+                                    context_lens=self.ctx[s], key=kk, value=v,
+                                    slot_mapping=self.slots[s])
 
     def gemv_chain(self) -> None:
         """Only the W8A16 linears of every step (4 per layer + lm_head), on static

@@ -3,7 +3,7 @@
 ``store_kvcache`` keeps the reference signature and asserts
 (attention.py:33-40) and runs the gfx950 slot-write kernel. ``Attention`` keeps
 the constructor and ``forward(q, k, v)`` contract (attention.py:43-82): write
-the new K/V rows through the slot mapping, then
+the new K/V rows through the slot mapping, then (both in one fused launch)
 
 * decode (``not context.is_prefill``): paged attention of one query row per
   sequence over ``context_lens`` keys; the output has flash-attn's
@@ -20,7 +20,6 @@ import torch
 from torch import nn
 
 from .. import ops
-from ..flash_attn_compat import flash_attn_varlen_func, flash_attn_with_kvcache
 from ..utils.context import get_context
 
 
@@ -42,22 +41,26 @@ class Attention(nn.Module):
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
-        if k_cache.numel() and v_cache.numel():
-            store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
-        if context.is_prefill:
-            if context.block_tables is None:
-                raise NotImplementedError("prefill over contiguous k/v is outside the decode "
-                                          "hot path served by this library")
-            return flash_attn_varlen_func(q, k_cache, v_cache,
-                                          max_seqlen_q=context.max_seqlen_q,
-                                          cu_seqlens_q=context.cu_seqlens_q,
-                                          max_seqlen_k=context.max_seqlen_k,
-                                          cu_seqlens_k=context.cu_seqlens_k,
-                                          softmax_scale=self.scale, causal=True,
-                                          block_table=context.block_tables)
-        # q is (B, Hq, D), or (Hq, D) when the batch holds one sequence.
-        q_in = q.unsqueeze(0).unsqueeze(0) if q.dim() == 2 else q.unsqueeze(1)
-        return flash_attn_with_kvcache(q_in, k_cache, v_cache,
-                                       cache_seqlens=context.context_lens,
-                                       block_table=context.block_tables,
-                                       softmax_scale=self.scale, causal=True)
+        has_cache = bool(k_cache.numel() and v_cache.numel())
+        if context.is_prefill and context.block_tables is None:
+            raise NotImplementedError("prefill over contiguous k/v is outside the decode "
+                                      "hot path served by this library")
+        if not has_cache:
+            raise RuntimeError("Attention needs its paged k_cache / v_cache")
+        # store_kvcache of k / v and the paged attention in one launch
+        if context.is_prefill:  # speculative verify / prefix-cache rows (attention.py:64-70)
+            return ops.paged_attention(q, k_cache, v_cache, context.block_tables, self.scale,
+                                       cu_seqlens_k=context.cu_seqlens_k,
+                                       cu_seqlens_q=context.cu_seqlens_q,
+                                       max_seqlen_q=int(context.max_seqlen_q),
+                                       key=k, value=v, slot_mapping=context.slot_mapping)
+        # decode (attention.py:71-81): q is (B, Hq, D), or (Hq, D) for one sequence;
+        # the result has flash_attn_with_kvcache's (B, 1, Hq, D) shape
+        if q.dim() == 2:
+            q, k, v = q.unsqueeze(0), k.reshape(1, *k.shape[-2:]), v.reshape(1, *v.shape[-2:])
+        if not (q.stride(-1) == 1 and q.stride(0) % 8 == 0 and q.stride(1) % 8 == 0):
+            q = q.contiguous()
+        o = ops.paged_attention(q, k_cache, v_cache, context.block_tables, self.scale,
+                                context_lens=context.context_lens,
+                                key=k, value=v, slot_mapping=context.slot_mapping)
+        return o.unsqueeze(1)

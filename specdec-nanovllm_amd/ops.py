@@ -87,7 +87,9 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
                     cu_seqlens_k: torch.Tensor | None = None,
                     cu_seqlens_q: torch.Tensor | None = None, max_seqlen_q: int = 1,
                     layout: str = "interleaved", num_splits: int = 0,
-                    out: torch.Tensor | None = None, main_only: bool = False) -> torch.Tensor:
+                    out: torch.Tensor | None = None, main_only: bool = False,
+                    key: torch.Tensor | None = None, value: torch.Tensor | None = None,
+                    slot_mapping: torch.Tensor | None = None) -> torch.Tensor:
     """Paged decode (``cu_seqlens_q is None``: one query row per sequence) or
     speculative-verify attention (rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]``,
     bottom-right causal), GQA, split-KV.
@@ -95,6 +97,12 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     q: (total_q, num_q_heads, head_dim); keys per sequence from ``context_lens``
     (B,) or ``cu_seqlens_k`` (B+1,). Returns ``out`` (same shape/dtype as q).
     ``main_only`` runs only the split-KV main kernel (measurement twin).
+
+    ``key``/``value`` (total_q, num_kv_heads, head_dim) with ``slot_mapping``
+    (total_q,): store_kvcache of these rows fused into the same launch — the
+    ``Attention.forward`` sequence (nanovllm/layers/attention.py:59-82). Same
+    cache and output as ``store_kvcache`` then attention, for the engine's slot
+    layout: sequence b's rows are its last n_b keys (slot -1: not written).
     """
     if q.dim() != 3:
         raise ValueError(f"q must be (tokens, heads, head_dim), got {tuple(q.shape)}")
@@ -125,18 +133,32 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         out = torch.empty_like(q)
     else:
         assert out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
-    if num_seqs == 0 or total_q == 0:
-        return out
+    fused = key is not None
+    if fused:
+        assert value is not None and slot_mapping is not None and not main_only
+        assert key.shape == (total_q, num_kv_heads, head_dim) and value.shape == key.shape
+        assert key.dtype == value.dtype == q.dtype
+        assert key.stride(-1) == 1 and value.stride(-1) == 1
+        assert slot_mapping.numel() == total_q
+        _lib.require_device(key, value, slot_mapping)
+    if total_q == 0 or (num_seqs == 0 and not fused):
+        return out  # (num_seqs == 0 with new rows: the library only stores them)
     lib = _lib.load()
     max_blocks = bt.shape[1]
     fn = lib.sd_paged_attention_partial if main_only else lib.sd_paged_attention
+    new_rows = ()
+    if fused:
+        slots = _i32(slot_mapping.reshape(-1))
+        fn = lib.sd_paged_attention_store
+        new_rows = (key.data_ptr(), key.stride(0), key.stride(1),
+                    value.data_ptr(), value.stride(0), value.stride(1), slots.data_ptr())
     with torch.cuda.device(dev):
         # the plan (and so the workspace) depends on the device's compute units
         ws_bytes = lib.sd_paged_attention_workspace_size(
             num_seqs, int(max_seqlen_q), num_q_heads, num_kv_heads, head_dim,
             max_blocks * block_size, int(num_splits))
         ws = _workspace(ws_bytes, dev)
-        rc = fn(q.data_ptr(), q.stride(0), q.stride(1),
+        rc = fn(*new_rows, q.data_ptr(), q.stride(0), q.stride(1),
                 k_cache.data_ptr(), v_cache.data_ptr(), sb, sp, sh, num_blocks,
                 block_size, bt.data_ptr(), bt.stride(0), max_blocks,
                 _ptr(ctx), _ptr(cuk), _ptr(cuq),

@@ -259,6 +259,129 @@ def test_hip_graph_replay_matches_eager():
                           what=f"graph replay {rep}")
 
 
+# ------------------------------------------------------------------ fused store
+def _fused_vs_separate(q, kc, vc, bt, knew, vnew, slots, scale, **kw):
+    kc1, vc1, kc2, vc2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    ops.store_kvcache(knew, vnew, kc1, vc1, slots)
+    o1 = ops.paged_attention(q, kc1, vc1, bt, scale, **kw)
+    o2 = ops.paged_attention(q, kc2, vc2, bt, scale, key=knew, value=vnew, slot_mapping=slots,
+                             **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), "fused store differs"
+    assert torch.equal(o1, o2), "fused attention differs from store-then-attend"
+    return o2, kc2, vc2
+
+
+@pytest.mark.parametrize("batch", [1, 8, 32])
+def test_fused_store_decode_is_store_then_attend(batch):
+    case = workloads.decode_case(batch, seed=300 + batch, num_blocks=512)
+    bt, lens, slots = case["tables"][0].to(DEV), case["lens"], case["slots"][0].to(DEV)
+    o, kc, vc = _fused_vs_separate(case["q"], case["k_cache"], case["v_cache"], bt,
+                                   case["k_new"], case["v_new"], slots, case["scale"],
+                                   context_lens=lens.to(DEV))
+    assert_close_attn(to_np(o), oracle(case["q"], kc, vc, case["tables"][0], lens, case["scale"]),
+                      what=f"fused decode B={batch}")
+
+
+def test_fused_store_verify_is_store_then_attend():
+    case = workloads.verify_case(seed=5, num_blocks=256)
+    o, kc, vc = _fused_vs_separate(case["q"], case["k_cache"], case["v_cache"],
+                                   case["table"].to(DEV), case["k_new"], case["v_new"],
+                                   case["slots"].to(DEV), case["scale"],
+                                   cu_seqlens_k=case["cu_k"].to(DEV),
+                                   cu_seqlens_q=case["cu_q"].to(DEV),
+                                   max_seqlen_q=case["k"] + 1)
+    ref = oracle(case["q"], kc, vc, case["table"], case["keys"], case["scale"], case["cu_q"])
+    assert_close_attn(to_np(o), ref, what="fused verify")
+
+
+def test_fused_store_pad_slots_and_small_pages():
+    # slot -1 rows (graph padding / rows not to write) keep the cache row as the key;
+    # 16-token pages take the per-lane page lookup path
+    for bs in (256, 16):
+        q, kc, vc, bt, lens = random_case([300, 1, 513, 40], bs=bs, seed=400 + bs)
+        g = torch.Generator().manual_seed(bs)
+        knew = torch.randn((4, 8, 128), generator=g).to(torch.bfloat16).to(DEV)
+        vnew = torch.randn((4, 8, 128), generator=g).to(torch.bfloat16).to(DEV)
+        slots = workloads.slots_for(bt, [[int(L) - 1] for L in lens], bs)
+        slots[1] = -1
+        slots[3] = -1
+        _fused_vs_separate(q, kc, vc, bt.to(DEV), knew, vnew, slots.to(DEV), 128 ** -0.5,
+                           context_lens=lens.to(DEV))
+
+
+def test_fused_store_more_rows_than_combine_threads():
+    # rows outside every sequence's query range (engine pad tokens with real
+    # slots) are still stored; 600 rows x 8 heads x 32 pieces is many times the
+    # combine grid, so the grid-stride copy loop runs
+    q, kc, vc, bt, lens = random_case([300, 700], hq=8, hkv=8, bs=16, seed=91, spare=40)
+    N = 600
+    g = torch.Generator().manual_seed(91)
+    q = torch.randn((N, 8, 128), generator=g).to(torch.bfloat16).to(DEV)
+    knew = torch.randn((N, 8, 128), generator=g).to(torch.bfloat16).to(DEV)
+    vnew = torch.randn((N, 8, 128), generator=g).to(torch.bfloat16).to(DEV)
+    slots = workloads.slots_for(bt, [[int(L) - 1] for L in lens], 16).tolist()
+    unused = sorted(set(range(kc.shape[0])) - set(int(x) for x in bt.flatten().tolist()))
+    slots += [blk * 16 + o for blk in unused for o in range(16)][:N - 2]
+    slots = torch.tensor(slots, dtype=torch.int32, device=DEV)
+    cu_q = torch.tensor([0, 1, 2], dtype=torch.int32, device=DEV)
+    cu_k = torch.tensor([0, 300, 1000], dtype=torch.int32, device=DEV)
+    kc1, vc1, kc2, vc2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    o1, o2 = torch.zeros_like(q), torch.zeros_like(q)
+    kw = dict(cu_seqlens_k=cu_k, cu_seqlens_q=cu_q, max_seqlen_q=1)
+    ops.store_kvcache(knew, vnew, kc1, vc1, slots)
+    ops.paged_attention(q, kc1, vc1, bt.to(DEV), 128 ** -0.5, out=o1, **kw)
+    ops.paged_attention(q, kc2, vc2, bt.to(DEV), 128 ** -0.5, out=o2, key=knew, value=vnew,
+                        slot_mapping=slots, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert torch.equal(o1, o2)
+
+
+def test_fused_store_without_sequences_only_stores():
+    kc = torch.zeros((4, 16, 8, 128), dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    g = torch.Generator().manual_seed(5)
+    knew = torch.randn((5, 8, 128), generator=g).to(torch.bfloat16).to(DEV)
+    vnew = torch.randn((5, 8, 128), generator=g).to(torch.bfloat16).to(DEV)
+    slots = torch.tensor([3, -1, 17, 63, 40], dtype=torch.int32, device=DEV)
+    kc1, vc1 = kc.clone(), vc.clone()
+    ops.store_kvcache(knew, vnew, kc1, vc1, slots)
+    ops.paged_attention(knew.clone(), kc, vc, torch.zeros((0, 1), dtype=torch.int32, device=DEV),
+                        128 ** -0.5, cu_seqlens_k=torch.zeros(1, dtype=torch.int32, device=DEV),
+                        cu_seqlens_q=torch.zeros(1, dtype=torch.int32, device=DEV),
+                        max_seqlen_q=1, key=knew, value=vnew, slot_mapping=slots)
+    torch.cuda.synchronize()
+    assert torch.equal(kc, kc1) and torch.equal(vc, vc1) and kc.abs().sum() > 0
+
+
+def test_fused_store_graph_replay():
+    case = workloads.decode_case(8, seed=77, num_blocks=256)
+    bt, lens, slots = case["tables"][0].to(DEV), case["lens"].to(DEV), case["slots"][0].to(DEV)
+    kc, vc, q = case["k_cache"], case["v_cache"], case["q"]
+    knew, vnew = case["k_new"], case["v_new"]
+    out = torch.empty_like(q)
+
+    def step():
+        ops.paged_attention(q, kc, vc, bt, case["scale"], context_lens=lens, out=out,
+                            key=knew, value=vnew, slot_mapping=slots)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
 # ------------------------------------------------------------- mirror entry points
 def test_mirror_entry_points_agree():
     q, kc, vc, bt, lens = random_case([1000, 2500, 1], seed=81)
