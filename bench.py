@@ -131,20 +131,24 @@ def cpu_baseline(case, seconds, torch):
     lens = case["lens"].tolist()
     hq, hkv, d = case["num_q_heads"], case["num_kv_heads"], case["head_dim"]
     q = case["q"].float().cpu().numpy()
+    host = {}  # sequence -> its pages on the host (copied once, outside the timing)
     done_bytes, spent, seqs = 0, 0.0, 0
     b = 0
-    while spent < seconds and seqs < 4 * len(lens):
+    while spent < seconds and seqs < 100000:
         L = lens[b]
-        pages = bt[b, :math.ceil(L / 256)].long().to(case["k_cache"].device)
-        kc = case["k_cache"][pages].float().cpu().numpy()
-        vc = case["v_cache"][pages].float().cpu().numpy()
-        table = np.arange(len(pages)).reshape(1, -1)
+        if b not in host:
+            pages = bt[b, :math.ceil(L / 256)].long().to(case["k_cache"].device)
+            host[b] = (case["k_cache"][pages].float().cpu().numpy(),
+                       case["v_cache"][pages].float().cpu().numpy(),
+                       np.arange(len(pages)).reshape(1, -1))
+        kc, vc, table = host[b]
         t0 = time.perf_counter()
         opa.paged_attention(q[b:b + 1], kc, vc, table, [L], case["scale"], dtype=np.float32)
         spent += time.perf_counter() - t0
         done_bytes += attn_bytes([L], hq, hkv, d, 2)
         seqs += 1
         b = (b + 1) % len(lens)
+    del host
     return {"value": round(done_bytes / spent / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"numpy fp32 oracle, {seqs} whole sequences of C2 B={len(lens)} "
