@@ -207,24 +207,34 @@ def bench_w8a16(ops, workloads, torch, steps):
 def bench_draft_chain(workloads_mod, torch, reps=5):
     """C5: hipGraph-captured k = 6 greedy draft steps of a random-init
     Qwen3-0.6B (28 layers, all linears W8A16, paged bf16 KV with a 2048-token
-    context) at B in {1, 16}: us per draft step, algorithmic GB/s, and the
-    shares of attention (store + paged attention) and of the W8A16 GEMVs, each
-    timed as its own graph over the same shapes."""
+    context) at B in {1, 16}, with the neighbour ops as eager torch (the C5
+    protocol) and as this library's fused kernels: us per draft step,
+    algorithmic GB/s, and the shares of attention (store + paged attention) and
+    of the W8A16 GEMVs, each timed as its own graph over the same shapes."""
     from specdec_nanovllm_amd.draft_chain import DraftChain
     rows = []
     for B in (1, 16):
         ch = DraftChain(B, ctx_len=2048, k=6, seed=B)
-        out = {"config": f"C5 draft chain B={B} ctx 2048 k=6"}
-        for name, fn in (("step", ch.chain), ("attention", ch.attention_chain),
-                         ("gemv", ch.gemv_chain)):
+        parts = {}
+        for name, fn in (("attention", ch.attention_chain), ("gemv", ch.gemv_chain)):
             g = graph_of(fn, torch)
-            out[f"{name}_us"] = round(time_replays([g], reps, 1, torch) * 1e3 / ch.k, 2)
-        out["GBps"] = round(ch.step_bytes() / out["step_us"] / 1e3, 1)
-        out["attention_share"] = round(out["attention_us"] / out["step_us"], 3)
-        out["gemv_share"] = round(out["gemv_us"] / out["step_us"], 3)
-        out["bytes_per_step"] = ch.step_bytes()
-        rows.append(out)
-        del ch, g
+            parts[name] = time_replays([g], reps, 1, torch) * 1e3 / ch.k
+            del g
+        for fused in (False, True):
+            ch.fused = fused
+            g = graph_of(ch.chain, torch)
+            step = time_replays([g], reps, 1, torch) * 1e3 / ch.k
+            del g
+            out = {"config": f"C5 draft chain B={B} ctx 2048 k=6, neighbours "
+                             + ("fused HIP kernels" if fused else "eager torch"),
+                   "step_us": round(step, 2), "attention_us": round(parts["attention"], 2),
+                   "gemv_us": round(parts["gemv"], 2),
+                   "GBps": round(ch.step_bytes() / step / 1e3, 1),
+                   "attention_share": round(parts["attention"] / step, 3),
+                   "gemv_share": round(parts["gemv"] / step, 3),
+                   "bytes_per_step": ch.step_bytes()}
+            rows.append(out)
+        del ch
         torch.cuda.empty_cache()
     return rows
 

@@ -200,6 +200,70 @@ int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t 
                     int64_t K, int32_t dtype, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Neighbours of the draft step (the row-wise work of a Qwen3 decoder step
+ * between the attention and linear launches). Eager-torch rounding: fp32
+ * arithmetic, a 16-bit rounding wherever the module converts to the
+ * activation dtype, no fused multiply-add where the module has none.
+ * ------------------------------------------------------------------------- */
+
+/*
+ * RMSNorm.forward (nanovllm/layers/layernorm.py:16-47). Per row of `hidden`:
+ *   residual == NULL: out = bf16(bf16(x * r) * weight), r = rsqrt(mean(x^2) + eps)
+ *   residual != NULL: s = x + residual (fp32); residual_out = bf16(s);
+ *                     out = bf16(bf16(s * r) * weight), r from s
+ * x/residual/out/residual_out: (rows, hidden) dtype, 16-byte aligned rows;
+ * out may alias x and residual_out may alias residual. hidden % 8 == 0,
+ * hidden <= 8192. weight: (hidden,) dtype.
+ */
+int sd_rmsnorm(const void* x, int64_t x_stride, const void* residual, int64_t residual_stride,
+               const void* weight, void* out, int64_t out_stride, void* residual_out,
+               int64_t residual_out_stride, int64_t rows, int32_t hidden, float eps,
+               int32_t dtype, void* stream);
+
+/*
+ * Per-head q/k RMSNorm then rotate-half RoPE, in place: Qwen3Attention.forward
+ * between the qkv projection and attention (nanovllm/models/qwen3.py:80-88)
+ * with RotaryEmbedding.forward (layers/rotary_embedding.py:6-48).
+ *   q: (num_tokens, num_q_heads, 128) by strides; k: (num_tokens, num_kv_heads, 128)
+ *   (views into the qkv projection output work); q_weight / k_weight: (128,)
+ *   dtype, NULL skips the norm (RoPE only).
+ *   positions: (num_tokens,) int64; cos_sin: (max_position, cos_sin_stride)
+ *   fp32 rows [cos(64) | sin(64)] — the reference's cos_sin_cache.
+ * A token whose position is outside [0, max_position) is left unchanged.
+ */
+int sd_qk_norm_rope(void* q, int64_t q_stride_tok, int64_t q_stride_head, void* k,
+                    int64_t k_stride_tok, int64_t k_stride_head, int64_t num_tokens,
+                    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                    const void* q_weight, const void* k_weight, float eps,
+                    const int64_t* positions, const float* cos_sin, int64_t cos_sin_stride,
+                    int64_t max_position, int32_t dtype, void* stream);
+
+/*
+ * SiluAndMul (nanovllm/layers/activation.py:6-11): x (rows, 2*width) = [gate | up],
+ * out (rows, width) = bf16(bf16(silu(gate)) * up). 16-byte aligned rows,
+ * width % 8 == 0.
+ */
+int sd_silu_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride, int64_t rows,
+                int32_t width, int32_t dtype, void* stream);
+
+/*
+ * Sampler.forward (nanovllm/layers/sampler.py:6-12; the draft's per-step
+ * sampling, spec_decode/draft_proposer.py:505-510): one token per row of
+ * logits (rows, vocab), dtype bf16/f16/f32, into out_tokens (rows,) int64.
+ *   temperatures == NULL, or a row's temperature <= 0: greedy argmax (first
+ *   index among equal maxima, as torch.argmax).
+ *   otherwise: argmax(softmax(l / T) / E), E ~ Exp(1), computed as
+ *   argmax(l / T - log E) with E = max(-log U, 1e-10), U in (0, 1] from
+ *   Philox4x32-10 keyed by rng_state[0] (seed) with counter (column,
+ *   row ^ high word of rng_state[1], low word of rng_state[1], 0).
+ *   rng_state: (2,) int64 on the device, read only; the caller advances the
+ *   offset between calls (on the stream, so graph replays advance it too).
+ */
+int sd_sample(const void* logits, int64_t logits_stride, int32_t dtype, int64_t rows,
+              int32_t vocab, const float* temperatures, const int64_t* rng_state,
+              int64_t* out_tokens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

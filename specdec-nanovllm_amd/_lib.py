@@ -56,6 +56,22 @@ SIGNATURES = {
         _i64, _i64, _i64, _i32,         # M, N, K, dtype
         _p, _sz, _p]),                  # workspace, bytes, stream
 }
+SIGNATURES.update({
+    "sd_rmsnorm": (ctypes.c_int, [
+        _p, _i64, _p, _i64,             # x, stride, residual, stride
+        _p, _p, _i64, _p, _i64,         # weight, out, stride, residual_out, stride
+        _i64, _i32, _f32, _i32, _p]),   # rows, hidden, eps, dtype, stream
+    "sd_qk_norm_rope": (ctypes.c_int, [
+        _p, _i64, _i64, _p, _i64, _i64,  # q, strides (tok, head), k, strides
+        _i64, _i32, _i32, _i32,         # tokens, hq, hkv, head_dim
+        _p, _p, _f32,                   # q_weight, k_weight, eps
+        _p, _p, _i64, _i64,             # positions, cos_sin, stride, max_position
+        _i32, _p]),                     # dtype, stream
+    "sd_silu_mul": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i32, _i32, _p]),
+    "sd_sample": (ctypes.c_int, [
+        _p, _i64, _i32, _i64, _i32,     # logits, stride, dtype, rows, vocab
+        _p, _p, _p, _p]),               # temperatures, rng_state, out_tokens, stream
+})
 SIGNATURES["sd_paged_attention_partial"] = SIGNATURES["sd_paged_attention"]
 SIGNATURES["sd_paged_attention_store"] = (ctypes.c_int, [
     _p, _i64, _i64,                 # key (new rows), strides (tok, head)

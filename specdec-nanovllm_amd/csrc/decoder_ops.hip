@@ -1,0 +1,447 @@
+// decoder_ops.hip — the draft step's neighbours of the attention and linear
+// kernels, for gfx950: the row-wise work of a Qwen3 decoder step that sits
+// between the library's paged attention and W8A16 launches.
+//
+//   rmsnorm_kernel       RMSNorm.forward, with or without the residual add
+//                        (nanovllm/layers/layernorm.py:16-47)
+//   qk_norm_rope_kernel  per-head q/k RMSNorm then rotate-half RoPE, in place
+//                        (models/qwen3.py:80-88, layers/rotary_embedding.py:6-48)
+//   silu_mul_kernel      SiluAndMul (layers/activation.py:6-11)
+//   sample_kernel        Sampler: temperature + exponential-race (Gumbel-max)
+//                        sampling, or greedy argmax (layers/sampler.py:6-12,
+//                        spec_decode/draft_proposer.py:505-510)
+//
+// Rounding follows the modules' eager torch semantics: fp32 arithmetic, a
+// 16-bit rounding wherever the module converts back to the activation dtype
+// (`x.to(orig_dtype)`, each elementwise op on 16-bit tensors), and no fused
+// multiply-add where the module has separate multiplies and adds.
+#include <math.h>
+
+#include "sd_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+template <typename T> __device__ __forceinline__ float ld(const uint16_t* p, int64_t i) {
+  return sd::from_bits<T>(p[i]);
+}
+template <typename T> __device__ __forceinline__ float round16(float x) {
+  return static_cast<float>(static_cast<T>(x));
+}
+
+// Block-wide fp32 sum (every thread gets it). `red` holds kThreads / 64 floats.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+  return s;
+}
+
+// ------------------------------------------------------------------ RMSNorm
+// One workgroup per row; thread t holds 8-element chunks t, t + 256, ...
+// (up to kChunks of them) in registers between the reduction and the writes,
+// so out / residual_out may alias x / residual.
+constexpr int kChunks = 4;  // hidden <= 8 * 256 * 4 = 8192
+
+struct NormParams {
+  const uint16_t* x;
+  int64_t xs;
+  const uint16_t* res;  // NULL: no residual add
+  int64_t rs;
+  const uint16_t* w;
+  uint16_t* out;
+  int64_t os;
+  uint16_t* res_out;
+  int64_t ros;
+  int32_t H;
+  float eps;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(NormParams p) {
+#pragma clang fp contract(off)
+  __shared__ float red[kThreads / 64];
+  const int64_t row = blockIdx.x;
+  const uint16_t* x = p.x + row * p.xs;
+  float v[kChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e0 = (c * kThreads + threadIdx.x) * 8;
+    if (e0 < p.H) {
+      const sd::u32x4 a = sd::load16(x + e0);
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+      sd::u32x4 b = {0u, 0u, 0u, 0u};
+      if (p.res) b = sd::load16(p.res + row * p.rs + e0);
+      const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float f = sd::from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
+        if (p.res) f = f + sd::from_bits<T>(static_cast<uint16_t>(bw[i / 2] >> (16 * (i & 1))));
+        v[c][i] = f;
+        ss += f * f;
+      }
+    }
+  }
+  const float var = block_sum(ss, red) / static_cast<float>(p.H);
+  const float r = rsqrtf(var + p.eps);
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e0 = (c * kThreads + threadIdx.x) * 8;
+    if (e0 < p.H) {
+      const sd::u32x4 wv = sd::load16(p.w + e0);
+      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t o[4], ro[4];
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const float w0 = sd::from_bits<T>(static_cast<uint16_t>(ww[i / 2]));
+        const float w1 = sd::from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> 16));
+        o[i / 2] = sd::pack2<T>(round16<T>(v[c][i] * r) * w0, round16<T>(v[c][i + 1] * r) * w1);
+        ro[i / 2] = sd::pack2<T>(v[c][i], v[c][i + 1]);
+      }
+      sd::store16(p.out + row * p.os + e0, sd::u32x4{o[0], o[1], o[2], o[3]});
+      if (p.res && p.res_out)
+        sd::store16(p.res_out + row * p.ros + e0, sd::u32x4{ro[0], ro[1], ro[2], ro[3]});
+    }
+  }
+}
+
+// ----------------------------------------------------------- q/k norm + RoPE
+// One wave per (token, head); lane l holds dims l and l + 64 of the 128, which
+// are exactly the pair rotate-half mixes, so RoPE needs no lane exchange.
+struct RopeParams {
+  uint16_t* q;
+  int64_t q_stok, q_shead;
+  uint16_t* k;
+  int64_t k_stok, k_shead;
+  int64_t tokens;
+  int32_t Hq, Hkv;
+  const uint16_t* qw;  // (128,) q_norm weight, NULL: no norm
+  const uint16_t* kw;
+  float eps;
+  const int64_t* pos;
+  const float* cos_sin;  // (max_position, cs_stride): cos[0:64] | sin[64:128]
+  int64_t cs_stride;
+  int64_t max_pos;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(RopeParams p) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  const int heads = p.Hq + p.Hkv;
+  if (item >= p.tokens * heads) return;
+  const int64_t t = item / heads;
+  const int hd = static_cast<int>(item - t * heads);
+  const bool is_q = hd < p.Hq;
+  uint16_t* x = is_q ? p.q + t * p.q_stok + static_cast<int64_t>(hd) * p.q_shead
+                     : p.k + t * p.k_stok + static_cast<int64_t>(hd - p.Hq) * p.k_shead;
+  const uint16_t* w = is_q ? p.qw : p.kw;
+  const int64_t pos = p.pos[t];
+  if (pos < 0 || pos >= p.max_pos) return;  // no cos/sin row: the head is left as it is
+  float x0 = ld<T>(x, lane), x1 = ld<T>(x, lane + 64);
+  if (w) {
+    float ss = x0 * x0 + x1 * x1;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float r = rsqrtf(ss / 128.f + p.eps);
+    x0 = round16<T>(round16<T>(x0 * r) * ld<T>(w, lane));
+    x1 = round16<T>(round16<T>(x1 * r) * ld<T>(w, lane + 64));
+  }
+  const float c = p.cos_sin[pos * p.cs_stride + lane];
+  const float s = p.cos_sin[pos * p.cs_stride + 64 + lane];
+  const float a = x0 * c, b = x1 * s;
+  const float e = x1 * c, f = x0 * s;
+  x[lane] = sd::to_bits<T>(a - b);
+  x[lane + 64] = sd::to_bits<T>(e + f);
+}
+
+// ----------------------------------------------------------------- SiLU * up
+// out[m, i] = bf16(bf16(silu(g)) * u), g = x[m, i], u = x[m, width + i].
+struct SiluParams {
+  const uint16_t* x;
+  int64_t xs;
+  uint16_t* out;
+  int64_t os;
+  int64_t rows;
+  int32_t width;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(SiluParams p) {
+#pragma clang fp contract(off)
+  const int64_t chunks = p.width / 8;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= p.rows * chunks) return;
+  const int64_t m = idx / chunks;
+  const int e0 = static_cast<int>(idx - m * chunks) * 8;
+  const sd::u32x4 g = sd::load16(p.x + m * p.xs + e0);
+  const sd::u32x4 u = sd::load16(p.x + m * p.xs + p.width + e0);
+  const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float r[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float gv = sd::from_bits<T>(static_cast<uint16_t>(gw[i] >> (16 * h)));
+      const float uv = sd::from_bits<T>(static_cast<uint16_t>(uw[i] >> (16 * h)));
+      const float sv = round16<T>(gv / (1.f + expf(-gv)));
+      r[h] = sv * uv;
+    }
+    o[i] = sd::pack2<T>(r[0], r[1]);
+  }
+  sd::store16(p.out + m * p.os + e0, sd::u32x4{o[0], o[1], o[2], o[3]});
+}
+
+// ------------------------------------------------------------------ sampling
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
+// as 1, 2, 3", SC 2011): counter (c0..c3), key (k0, k1), ten rounds.
+__device__ __forceinline__ void philox(uint32_t c[4], uint32_t k0, uint32_t k1) {
+  constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+  constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = static_cast<uint64_t>(M0) * c[0];
+    const uint64_t p1 = static_cast<uint64_t>(M1) * c[2];
+    const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c[1] ^ k0;
+    const uint32_t n1 = static_cast<uint32_t>(p1);
+    const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c[3] ^ k1;
+    const uint32_t n3 = static_cast<uint32_t>(p0);
+    c[0] = n0;
+    c[1] = n1;
+    c[2] = n2;
+    c[3] = n3;
+    k0 += W0;
+    k1 += W1;
+  }
+}
+
+struct SampleParams {
+  const void* logits;
+  int64_t ls;
+  int32_t dtype;  // SD_BF16 / SD_F16 / SD_F32
+  int32_t V;
+  const float* temp;      // (rows,), NULL: greedy
+  const int64_t* state;   // (2,) device: seed, offset; read only
+  int64_t* out;
+};
+
+constexpr int kSampleThreads = 1024;
+
+__device__ __forceinline__ float logit_at(const SampleParams& p, int64_t row, int i) {
+  if (p.dtype == SD_F32) return static_cast<const float*>(p.logits)[row * p.ls + i];
+  const uint16_t b = static_cast<const uint16_t*>(p.logits)[row * p.ls + i];
+  return p.dtype == SD_BF16 ? sd::from_bits<__bf16>(b) : sd::from_bits<_Float16>(b);
+}
+
+// Better (key, index): larger key, or the same key at a smaller index (the
+// first maximum, as torch.argmax).
+__device__ __forceinline__ bool better(float k, int i, float bk, int bi) {
+  return k > bk || (k == bk && i < bi);
+}
+
+// One workgroup per row. Greedy: argmax of the logits. Sampled (T > 0): the
+// reference's argmax(softmax(l / T) / E) with E ~ Exp(1) is the argmax of
+// l / T - log(E) (log is monotone and the softmax normaliser is common to the
+// row), so one pass suffices. E = -log(U), U uniform in (0, 1] from Philox
+// with key = seed and counter = (column, row, offset).
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) {
+  __shared__ float sk[kSampleThreads / 64];
+  __shared__ int si[kSampleThreads / 64];
+  const int64_t row = blockIdx.x;
+  const float T = p.temp ? p.temp[row] : 0.f;
+  const bool greedy = !(T > 0.f);
+  const float inv_t = greedy ? 1.f : 1.f / T;
+  uint32_t k0 = 0, k1 = 0, off0 = 0, off1 = 0;
+  if (!greedy) {
+    const uint64_t seed = static_cast<uint64_t>(p.state[0]);
+    const uint64_t off = static_cast<uint64_t>(p.state[1]);
+    k0 = static_cast<uint32_t>(seed);
+    k1 = static_cast<uint32_t>(seed >> 32);
+    off0 = static_cast<uint32_t>(off);
+    off1 = static_cast<uint32_t>(off >> 32);
+  }
+  float bk = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < p.V; i += kSampleThreads) {
+    float key = logit_at(p, row, i);
+    if (!greedy) {
+      uint32_t c[4] = {static_cast<uint32_t>(i), static_cast<uint32_t>(row) ^ off1, off0, 0u};
+      philox(c, k0, k1);
+      const float u = (static_cast<float>(c[0] >> 8) + 1.f) * (1.f / 16777216.f);  // (0, 1]
+      const float e = fmaxf(-logf(u), 1e-10f);
+      key = key * inv_t - logf(e);
+    }
+    if (better(key, i, bk, bi)) {
+      bk = key;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ok = __shfl_xor(bk, off);
+    const int oi = __shfl_xor(bi, off);
+    if (better(ok, oi, bk, bi)) {
+      bk = ok;
+      bi = oi;
+    }
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) {
+    sk[wave] = bk;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kSampleThreads / 64; ++w)
+      if (better(sk[w], si[w], bk, bi)) {
+        bk = sk[w];
+        bi = si[w];
+      }
+    p.out[row] = bi == 0x7fffffff ? 0 : bi;  // an all-NaN row gives token 0
+  }
+}
+
+bool is16(int32_t dtype) { return dtype == SD_BF16 || dtype == SD_F16; }
+
+}  // namespace
+
+extern "C" int sd_rmsnorm(const void* x, int64_t x_stride, const void* residual,
+                          int64_t residual_stride, const void* weight, void* out,
+                          int64_t out_stride, void* residual_out, int64_t residual_out_stride,
+                          int64_t rows, int32_t hidden, float eps, int32_t dtype, void* stream) {
+  sd::clear_error();
+  if (rows < 0 || hidden <= 0 || hidden % 8 != 0 || hidden > 8 * kThreads * kChunks ||
+      !is16(dtype)) {
+    sd::set_error("rmsnorm: hidden must be a multiple of 8 up to %d, dtype bf16/fp16 "
+                  "(rows=%lld hidden=%d dtype=%d)", 8 * kThreads * kChunks, (long long)rows,
+                  hidden, dtype);
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (rows == 0) return SD_OK;
+  if (!x || !weight || !out || (residual && !residual_out)) {
+    sd::set_error("rmsnorm: null pointer argument");
+    return SD_ERR_VALUE;
+  }
+  if (!sd::aligned16(x) || !sd::aligned16(weight) || !sd::aligned16(out) ||
+      (residual && (!sd::aligned16(residual) || !sd::aligned16(residual_out))) ||
+      x_stride % 8 || out_stride % 8 || (residual && (residual_stride % 8 || residual_out_stride % 8))) {
+    sd::set_error("rmsnorm: rows must be 16-byte aligned");
+    return SD_ERR_UNSUPPORTED;
+  }
+  NormParams p{static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(residual),
+               residual_stride, static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
+               out_stride, static_cast<uint16_t*>(residual_out), residual_out_stride, hidden, eps};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows > 0x7fffffff) {
+    sd::set_error("rmsnorm: too many rows (%lld)", (long long)rows);
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (dtype == SD_BF16)
+    hipLaunchKernelGGL(rmsnorm_kernel<__bf16>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<_Float16>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, st, p);
+  return sd::check_launch("rmsnorm");
+}
+
+extern "C" int sd_qk_norm_rope(void* q, int64_t q_stride_tok, int64_t q_stride_head, void* k,
+                               int64_t k_stride_tok, int64_t k_stride_head, int64_t num_tokens,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               const void* q_weight, const void* k_weight, float eps,
+                               const int64_t* positions, const float* cos_sin,
+                               int64_t cos_sin_stride, int64_t max_position, int32_t dtype,
+                               void* stream) {
+  sd::clear_error();
+  if (head_dim != 128 || !is16(dtype) || num_tokens < 0 || num_q_heads < 0 || num_kv_heads < 0 ||
+      max_position <= 0 || cos_sin_stride < 128) {
+    sd::set_error("qk_norm_rope: head_dim 128 and bf16/fp16 only, cos_sin rows of >= 128 "
+                  "floats (head_dim=%d dtype=%d stride=%lld)", head_dim, dtype,
+                  (long long)cos_sin_stride);
+    return SD_ERR_UNSUPPORTED;
+  }
+  const int64_t items = num_tokens * (num_q_heads + num_kv_heads);
+  if (items == 0) return SD_OK;
+  if ((num_q_heads && !q) || (num_kv_heads && !k) || !positions || !cos_sin) {
+    sd::set_error("qk_norm_rope: null pointer argument");
+    return SD_ERR_VALUE;
+  }
+  const int64_t wgs = (items + kThreads / 64 - 1) / (kThreads / 64);
+  if (wgs > 0x7fffffff) {
+    sd::set_error("qk_norm_rope: too many heads (%lld)", (long long)items);
+    return SD_ERR_UNSUPPORTED;
+  }
+  RopeParams p{static_cast<uint16_t*>(q), q_stride_tok, q_stride_head, static_cast<uint16_t*>(k),
+               k_stride_tok, k_stride_head, num_tokens, num_q_heads, num_kv_heads,
+               static_cast<const uint16_t*>(q_weight), static_cast<const uint16_t*>(k_weight), eps,
+               positions, cos_sin, cos_sin_stride, max_position};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SD_BF16)
+    hipLaunchKernelGGL(qk_norm_rope_kernel<__bf16>, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_kernel<_Float16>, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0, st, p);
+  return sd::check_launch("qk_norm_rope");
+}
+
+extern "C" int sd_silu_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride,
+                           int64_t rows, int32_t width, int32_t dtype, void* stream) {
+  sd::clear_error();
+  if (rows < 0 || width <= 0 || width % 8 || !is16(dtype)) {
+    sd::set_error("silu_mul: width must be a positive multiple of 8, dtype bf16/fp16 "
+                  "(width=%d dtype=%d)", width, dtype);
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (rows == 0) return SD_OK;
+  if (!x || !out) {
+    sd::set_error("silu_mul: null pointer argument");
+    return SD_ERR_VALUE;
+  }
+  if (!sd::aligned16(x) || !sd::aligned16(out) || x_stride % 8 || out_stride % 8) {
+    sd::set_error("silu_mul: rows must be 16-byte aligned");
+    return SD_ERR_UNSUPPORTED;
+  }
+  const int64_t wgs = (rows * (width / 8) + kThreads - 1) / kThreads;
+  if (wgs > 0x7fffffff) {
+    sd::set_error("silu_mul: too large (%lld rows)", (long long)rows);
+    return SD_ERR_UNSUPPORTED;
+  }
+  SiluParams p{static_cast<const uint16_t*>(x), x_stride, static_cast<uint16_t*>(out), out_stride,
+               rows, width};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SD_BF16)
+    hipLaunchKernelGGL(silu_mul_kernel<__bf16>, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL(silu_mul_kernel<_Float16>, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0, st, p);
+  return sd::check_launch("silu_mul");
+}
+
+extern "C" int sd_sample(const void* logits, int64_t logits_stride, int32_t dtype, int64_t rows,
+                         int32_t vocab, const float* temperatures, const int64_t* rng_state,
+                         int64_t* out_tokens, void* stream) {
+  sd::clear_error();
+  if (rows < 0 || vocab <= 0 || (dtype != SD_BF16 && dtype != SD_F16 && dtype != SD_F32)) {
+    sd::set_error("sample: vocab must be positive, logits bf16/fp16/fp32 (vocab=%d dtype=%d)",
+                  vocab, dtype);
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (rows == 0) return SD_OK;
+  if (!logits || !out_tokens || (temperatures && !rng_state)) {
+    sd::set_error("sample: null pointer argument (temperatures need rng_state)");
+    return SD_ERR_VALUE;
+  }
+  if (rows > 0x7fffffff) {
+    sd::set_error("sample: too many rows (%lld)", (long long)rows);
+    return SD_ERR_UNSUPPORTED;
+  }
+  SampleParams p{logits, logits_stride, dtype, vocab, temperatures, rng_state, out_tokens};
+  hipLaunchKernelGGL(sample_kernel, dim3(static_cast<unsigned>(rows)), dim3(kSampleThreads), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return sd::check_launch("sample");
+}

@@ -14,8 +14,11 @@ position is ``ctx_len + s``, the slot ``bt[pos // 256] * 256 + pos % 256`` and
 the key count ``pos + 1``; the layers call ``store_kvcache``, paged decode
 attention and the W8A16 linears of this library, and the next token is the
 argmax of the logits (the greedy draft). The hot-path ops run on the gfx950
-kernels; RMSNorm, RoPE, SiLU*mul, the embedding lookup and the argmax are plain
-eager torch (no torch.compile), as the neighbours of the path.
+kernels. The neighbours of the path — RMSNorm (+ residual add), q/k norm +
+RoPE, SiLU*mul and the argmax — are plain eager torch (no torch.compile) with
+``fused=False``, or this library's fused neighbour kernels with ``fused=True``
+(q/k norm + RoPE in place on the qkv output, which the attention reads through
+strides; the embedding lookup stays a torch index).
 
 ``chain()`` runs ``k`` steps back to back, each feeding its tokens to the next,
 on static buffers, so the whole chain can be captured in one HIP graph.
@@ -40,8 +43,9 @@ class DraftChain:
                  hidden: int = 1024, heads: int = 16, kv_heads: int = 8, head_dim: int = 128,
                  inter: int = 3072, vocab: int = 151936, theta: float = 1e6, eps: float = 1e-6,
                  block_size: int = 256, seed: int = 0, device="cuda",
-                 dtype: torch.dtype = torch.bfloat16):
+                 dtype: torch.dtype = torch.bfloat16, fused: bool = False):
         self.B, self.ctx_len, self.k = batch, ctx_len, k
+        self.fused = fused
         self.L, self.H, self.Hq, self.Hkv, self.D = layers, hidden, heads, kv_heads, head_dim
         self.I, self.V, self.eps, self.bs = inter, vocab, eps, block_size
         self.dev, self.dtype = torch.device(device), dtype
@@ -74,6 +78,7 @@ class DraftChain:
         pos = torch.arange(ctx_len + k + 1, dtype=torch.float32, device=self.dev)
         freqs = pos[:, None] * inv_freq[None, :]
         self.cos, self.sin = freqs.cos(), freqs.sin()
+        self.cos_sin = torch.cat((self.cos, self.sin), dim=-1).contiguous()  # [cos | sin]
 
         # paged KV cache: (2, layers, blocks, bs, Hkv, D), a synthetic prefilled
         # context of ctx_len rows per sequence; pages are a seeded shuffle
@@ -116,7 +121,9 @@ class DraftChain:
 
     # ----------------------------------------------------------------------- step
     def step(self, s: int) -> torch.Tensor:
-        """Draft step s: reads tokens[s], writes and returns tokens[s + 1]."""
+        """Draft step s: reads tokens[s], writes tokens[s + 1], returns the logits."""
+        if self.fused:
+            return self._step_fused(s)
         B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
         pos = self.positions[s]
         cos, sin = self.cos[pos], self.sin[pos]
@@ -147,6 +154,33 @@ class DraftChain:
         logits = ops.w8a16_linear(x, *self.lm_head)
         nxt = logits.argmax(dim=-1)
         self.tokens[s + 1].copy_(nxt)
+        return logits
+
+    def _step_fused(self, s: int) -> torch.Tensor:
+        B, Hq, Hkv, D, eps = self.B, self.Hq, self.Hkv, self.D, self.eps
+        pos, slots, ctx = self.positions[s], self.slots[s], self.ctx[s]
+        h = self.embed[self.tokens[s]]
+        residual = None
+        for li, lw in enumerate(self.layers):
+            if residual is None:
+                residual = h
+                x = ops.rmsnorm(h, lw["in_norm"], eps)
+            else:
+                x, residual = ops.rmsnorm(h, lw["in_norm"], eps, residual=residual)
+            qkv = ops.w8a16_linear(x, *lw["qkv"])
+            q = qkv[:, :Hq * D].view(B, Hq, D)
+            kk = qkv[:, Hq * D:(Hq + Hkv) * D].view(B, Hkv, D)
+            v = qkv[:, (Hq + Hkv) * D:].view(B, Hkv, D)
+            ops.qk_norm_rope(q, kk, pos, self.cos_sin, lw["q_norm"], lw["k_norm"], eps)
+            o = ops.paged_attention(q, self.kv[0, li], self.kv[1, li], self.block_table,
+                                    self.scale, context_lens=ctx, key=kk, value=v,
+                                    slot_mapping=slots)
+            h = ops.w8a16_linear(o.reshape(B, Hq * D), *lw["o"])
+            x, residual = ops.rmsnorm(h, lw["post_norm"], eps, residual=residual)
+            h = ops.w8a16_linear(ops.silu_mul(ops.w8a16_linear(x, *lw["gate_up"])), *lw["down"])
+        x, _ = ops.rmsnorm(h, self.final_norm, eps, residual=residual)
+        logits = ops.w8a16_linear(x, *self.lm_head)
+        ops.sample(logits, out=self.tokens[s + 1])
         return logits
 
     def chain(self) -> None:

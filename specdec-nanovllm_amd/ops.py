@@ -213,3 +213,124 @@ def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
             _ptr(ws), ws_bytes, _lib.stream_ptr(dev))
     _lib.check(rc)
     return y.view(*x.shape[:-1], N)
+
+
+# --------------------------------------------------------------- draft-step neighbours
+def _rows16(t: torch.Tensor, what: str) -> torch.Tensor:
+    """2-D (rows, width) view with a unit last stride and 16-byte aligned rows."""
+    t2 = t.reshape(-1, t.shape[-1])
+    if t2.stride(-1) != 1 or t2.data_ptr() % 16 or (t2.shape[0] > 1 and t2.stride(0) % 8):
+        t2 = t2.contiguous()
+    return t2
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """RMSNorm.forward (nanovllm/layers/layernorm.py:16-47) over the last dim.
+
+    ``residual is None``: returns ``bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight)``.
+    Otherwise returns ``(out, residual_out)`` with ``s = x + residual`` in fp32,
+    ``residual_out = s`` rounded to the dtype and ``out`` the norm of ``s``.
+    """
+    H = x.shape[-1]
+    x2 = _rows16(x, "x")
+    assert weight.shape == (H,), "weight must be (hidden,)"
+    w = weight.to(x.dtype).contiguous()
+    r2 = None if residual is None else _rows16(residual, "residual")
+    if r2 is not None:
+        assert residual.shape == x.shape and residual.dtype == x.dtype
+    dev = _lib.require_device(x2, w, r2, out)
+    o = torch.empty_like(x2) if out is None else out.reshape(-1, H)
+    ro = None if r2 is None else torch.empty_like(r2)
+    rows = x2.shape[0]
+    if rows:
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            rc = lib.sd_rmsnorm(x2.data_ptr(), x2.stride(0), _ptr(r2), 0 if r2 is None else r2.stride(0),
+                                w.data_ptr(), o.data_ptr(), o.stride(0), _ptr(ro),
+                                0 if ro is None else ro.stride(0), rows, H, float(eps),
+                                _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
+        _lib.check(rc)
+    o = o.view(x.shape)
+    if residual is None:
+        return o
+    return o, ro.view(x.shape)
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor,
+                 cos_sin_cache: torch.Tensor, q_weight: torch.Tensor | None = None,
+                 k_weight: torch.Tensor | None = None, eps: float = 1e-6) -> None:
+    """In place on q (T, Hq, 128) and k (T, Hkv, 128) (strided views allowed):
+    per-head RMSNorm with q_weight / k_weight (skipped when None), then
+    rotate-half RoPE at ``positions`` from ``cos_sin_cache`` (max_pos, [1,] 128)
+    fp32 = [cos | sin] (nanovllm/models/qwen3.py:80-88,
+    layers/rotary_embedding.py:6-48)."""
+    assert q.dim() == 3 and k.dim() == 3 and q.shape[0] == k.shape[0]
+    assert q.shape[-1] == 128 and k.shape[-1] == 128 and q.stride(-1) == 1 and k.stride(-1) == 1
+    assert q.dtype == k.dtype
+    assert (q_weight is None) == (k_weight is None)
+    T = q.shape[0]
+    cs = cos_sin_cache.reshape(cos_sin_cache.shape[0], -1)
+    assert cs.dtype == torch.float32 and cs.shape[1] >= 128 and cs.stride(-1) == 1
+    pos = positions.reshape(-1)
+    if pos.dtype != torch.int64:
+        pos = pos.to(torch.int64)
+    pos = pos.contiguous()
+    assert pos.numel() == T
+    qw = None if q_weight is None else q_weight.to(q.dtype).contiguous()
+    kw = None if k_weight is None else k_weight.to(q.dtype).contiguous()
+    dev = _lib.require_device(q, k, pos, cs, qw, kw)
+    if T == 0:
+        return
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.sd_qk_norm_rope(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+                                 k.stride(1), T, q.shape[1], k.shape[1], 128, _ptr(qw), _ptr(kw),
+                                 float(eps), pos.data_ptr(), cs.data_ptr(), cs.stride(0),
+                                 cs.shape[0], _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
+    _lib.check(rc)
+
+
+def silu_mul(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """SiluAndMul (nanovllm/layers/activation.py:6-11): x (..., 2I) -> (..., I)."""
+    W = x.shape[-1]
+    assert W % 2 == 0
+    x2 = _rows16(x, "x")
+    dev = _lib.require_device(x2, out)
+    o = torch.empty((x2.shape[0], W // 2), dtype=x.dtype, device=dev) if out is None \
+        else out.reshape(-1, W // 2)
+    if x2.shape[0]:
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            rc = lib.sd_silu_mul(x2.data_ptr(), x2.stride(0), o.data_ptr(), o.stride(0),
+                                 x2.shape[0], W // 2, _lib.dtype_code(x.dtype),
+                                 _lib.stream_ptr(dev))
+        _lib.check(rc)
+    return o.view(*x.shape[:-1], W // 2)
+
+
+def sample(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
+           rng_state: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One token per row of logits (rows, vocab): greedy argmax when
+    ``temperatures`` is None (or a row's temperature is <= 0), otherwise the
+    exponential-race draw of ``Sampler.forward`` (nanovllm/layers/sampler.py:6-12)
+    with Philox noise keyed by ``rng_state`` = (seed, offset) int64 on the device.
+    The caller advances ``rng_state[1]`` between draws."""
+    assert logits.dim() == 2 and logits.stride(-1) == 1
+    rows, V = logits.shape
+    t = None
+    if temperatures is not None:
+        t = temperatures.reshape(-1).to(torch.float32).contiguous()
+        assert t.numel() == rows and rng_state is not None and rng_state.numel() == 2
+        assert rng_state.dtype == torch.int64
+    dev = _lib.require_device(logits, t, rng_state, out)
+    o = torch.empty(rows, dtype=torch.int64, device=dev) if out is None else out
+    assert o.dtype == torch.int64 and o.numel() == rows and o.is_contiguous()
+    if rows:
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            rc = lib.sd_sample(logits.data_ptr(), logits.stride(0), _lib.dtype_code(logits.dtype),
+                               rows, V, _ptr(t), _ptr(rng_state), o.data_ptr(),
+                               _lib.stream_ptr(dev))
+        _lib.check(rc)
+    return o

@@ -4,6 +4,8 @@ torch float32 restatement of the same decoder step: dequantized weights
 rounding points between ops. Floating point: logits of every step must agree to
 ``max|got - ref| <= 2e-2 * max|ref|`` (bf16 activations between ops), and the
 HIP-graph replay of the chain must reproduce the eager chain bit for bit.
+Both forms of the step are covered: eager-torch neighbours and this library's
+fused neighbour kernels.
 """
 import pytest
 import torch
@@ -74,23 +76,28 @@ def ref_step(ch: DraftChain, kv: torch.Tensor, tokens: torch.Tensor, s: int) -> 
     return (x.float() @ dequantize_weight(*ch.lm_head).T)
 
 
-def test_draft_chain_matches_float32_reference():
-    ch = DraftChain(3, **SMALL)
+@pytest.mark.parametrize("fused", [False, True])
+def test_draft_chain_matches_float32_reference(fused):
+    ch = DraftChain(3, fused=fused, **SMALL)
     kv_ref = ch.kv.clone()
     logits = []
     for s in range(ch.k):
         logits.append(ch.step(s).float())
+    tokens = ch.tokens.clone()
     torch.cuda.synchronize()
     for s in range(ch.k):
         ref = ref_step(ch, kv_ref, ch.tokens[s], s)
         err = (logits[s] - ref).abs().max().item()
         assert err <= 2e-2 * ref.abs().max().item(), f"step {s}: max err {err:.4g}"
+        # the drafted token is the argmax of the step's own logits
+        assert torch.equal(tokens[s + 1], logits[s].argmax(dim=-1))
     # the new K/V rows landed where the reference put them
     assert torch.equal(ch.kv, kv_ref) or (ch.kv.float() - kv_ref.float()).abs().max() < 5e-2
 
 
-def test_draft_chain_graph_replay_is_bitwise_eager():
-    ch = DraftChain(2, **SMALL)
+@pytest.mark.parametrize("fused", [False, True])
+def test_draft_chain_graph_replay_is_bitwise_eager(fused):
+    ch = DraftChain(2, fused=fused, **SMALL)
     kv0, tok0 = ch.kv.clone(), ch.tokens.clone()
     ch.chain()
     torch.cuda.synchronize()
