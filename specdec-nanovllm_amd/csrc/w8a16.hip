@@ -362,20 +362,27 @@ int w8_device_cus() {
 
 W8Plan make_plan(int64_t M, int64_t N, int64_t K) {
   W8Plan pl;
-  pl.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  // Activation rows in blocks of 16 (MT = 1) or 32 (MT = 2) along grid.y: a
+  // 64-row tile needs more registers than 2 waves per SIMD allow. The blocks
+  // of one row group run at the same time on the same XCD (launch_k sizes the
+  // grid to one resident set with grid.x a multiple of 8), so mostly only the
+  // first reads the weights from HBM; the others hit L2.
+  pl.MT = M <= 16 ? 1 : 2;
   pl.mblocks = static_cast<int>((M + pl.MT * 16 - 1) / (pl.MT * 16));
   const int64_t nr = (N + 15) / 16;
   const int cus = w8_device_cus();
   const int64_t nks = K / 64;
   // Enough 16-row tiles for ~8 waves per CU: every wave owns whole rows, two
-  // (MT <= 2) or four tiles at a time. Otherwise four waves split K of one tile.
+  // tiles at a time. Otherwise four waves split K of one tile (16 activation
+  // rows: the measured best for the narrow layers at every M).
   if (nr * pl.mblocks >= 8ll * cus || nks < 4) {
     pl.KW = 1;
-    pl.NT = pl.MT == 4 ? 4 : 2;
-    if (nr < pl.NT) pl.NT = 1;
+    pl.NT = nr < 2 ? 1 : 2;
   } else {
     pl.KW = 4;
     pl.NT = 1;
+    pl.MT = 1;
+    pl.mblocks = static_cast<int>((M + 15) / 16);
   }
   pl.groups = static_cast<int>((nr + pl.NT - 1) / pl.NT);
   const int nsub = kWaves / pl.KW;
@@ -402,9 +409,11 @@ template <typename T, int MT, int NT, int KW, bool PG>
 void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
   constexpr int U = NT >= 2 ? 2 : 4;  // 64-k steps per chunk
   auto kern = w8a16_kernel<T, MT, NT, KW, U, PG>;
-  // exactly one resident set of workgroups: a partial second round would
-  // leave most of the GPU idle at the end
-  const unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs(kern));
+  // exactly one resident set of workgroups over all activation blocks (a
+  // partial second round would leave most of the GPU idle at the end), grid.x
+  // a multiple of 8 so that block (x, y) shares an XCD (and its L2) with (x, 0)
+  unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs(kern)) / grid.y;
+  cap = cap >= 8 ? cap / 8 * 8 : 1;
   if (grid.x > cap) grid.x = cap;
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, p);
 }
@@ -416,16 +425,10 @@ void launch_kw(const W8Params& p, const W8Plan& pl, dim3 grid, hipStream_t st) {
       case 1 * 8 + 1: launch_k<T, 1, 1, 1, PG>(p, grid, st); break;
       case 1 * 8 + 2: launch_k<T, 1, 2, 1, PG>(p, grid, st); break;
       case 2 * 8 + 1: launch_k<T, 2, 1, 1, PG>(p, grid, st); break;
-      case 2 * 8 + 2: launch_k<T, 2, 2, 1, PG>(p, grid, st); break;
-      case 4 * 8 + 1: launch_k<T, 4, 1, 1, PG>(p, grid, st); break;
-      default: launch_k<T, 4, 4, 1, PG>(p, grid, st); break;
+      default: launch_k<T, 2, 2, 1, PG>(p, grid, st); break;
     }
   } else {
-    switch (pl.MT) {
-      case 1: launch_k<T, 1, 1, KW, PG>(p, grid, st); break;
-      case 2: launch_k<T, 2, 1, KW, PG>(p, grid, st); break;
-      default: launch_k<T, 4, 1, KW, PG>(p, grid, st); break;
-    }
+    launch_k<T, 1, 1, KW, PG>(p, grid, st);  // make_plan sets MT = 1 with KW > 1
   }
 }
 
