@@ -204,6 +204,26 @@ def bench_w8a16(ops, workloads, torch, steps):
     return rows
 
 
+def bench_verify_batch(ops, torch, steps):
+    """Rejection-sampling verification (spec_decode/verify.py) at the C3 verify
+    shape: B = 8 sequences, k = 6 draft tokens, vocab 151936, fp32 draft and
+    target logits. Bytes: every logit once (row statistics) + the two rows the
+    residual race rereads per sequence."""
+    B, k, V = 8, 6, 151936
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    tl = torch.randn((B, k + 1, V), generator=g, device="cuda") * 3
+    dl = tl[:, :k] + torch.randn((B, k, V), generator=g, device="cuda")
+    toks = torch.randint(0, V, (B, k), generator=g, device="cuda")
+    temps = torch.ones(B, device="cuda")
+    st = torch.tensor([1, 0], dtype=torch.int64, device="cuda")
+    g_ = graph_of(lambda: ops.verify_batch(dl, tl, toks, temps, rng_state=st), torch)
+    ms = time_replays([g_], steps, 5, torch)
+    nbytes = B * (2 * k + 1) * V * 4 + B * 2 * V * 4
+    return {"config": "verify_batch B=8 k=6 vocab 151936 fp32 logits", "us": round(ms * 1e3, 2),
+            "GBps": round(nbytes / ms / 1e6, 1), "bytes": nbytes}
+
+
 def bench_draft_chain(workloads_mod, torch, reps=5):
     """C5: hipGraph-captured k = 6 greedy draft steps of a random-init
     Qwen3-0.6B (28 layers, all linears W8A16, paged bf16 KV with a 2048-token
@@ -366,6 +386,8 @@ def main():
         extra["verify"] = bench_verify(ops, workloads, torch, args.steps)
         torch.cuda.empty_cache()
         extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100))
+        torch.cuda.empty_cache()
+        extra["verify_batch"] = bench_verify_batch(ops, torch, min(args.steps, 100))
         torch.cuda.empty_cache()
         if not args.no_draft_chain:
             extra["draft_chain"] = bench_draft_chain(workloads, torch)

@@ -264,6 +264,41 @@ int sd_sample(const void* logits, int64_t logits_stride, int32_t dtype, int64_t 
               int32_t vocab, const float* temperatures, const int64_t* rng_state,
               int64_t* out_tokens, void* stream);
 
+/*
+ * Workspace bytes of sd_verify_batch (0 for an empty batch).
+ */
+size_t sd_verify_batch_workspace_size(int64_t batch, int32_t k, int32_t vocab);
+
+/*
+ * Speculative verification by rejection sampling: `verify_batch`
+ * (nanovllm/spec_decode/verify.py:39-183).
+ *   draft   : (batch, k, vocab) by strides, bf16/f16/f32: the draft's raw logits
+ *             (q_j = softmax(draft_j / T)), or its probabilities when
+ *             draft_is_point_mass != 0 (the n-gram route; used as given)
+ *   target  : (batch, k + 1, vocab) by strides: the target's logits
+ *             (p_j = softmax(target_j / T))
+ *   draft_tokens : (batch, k) int64, row stride tokens_stride_b
+ *   temperatures : (batch,) fp32 or NULL (1); a temperature <= 0 is taken as 1
+ *   rng_state    : (2,) int64 on the device: seed, offset (read only; the
+ *                  caller advances the offset between calls)
+ * Outputs: accepted (batch,) int64 = index of the first rejected candidate (k
+ * when all pass; candidate j passes when u_j < min(1, p_j[x_j] / q_j[x_j]),
+ * 0 when q_j[x_j] == 0); bonus (batch,) int64 drawn from
+ * normalize(max(0, p_a - q_a)) at a = accepted with q_k = 0 (p_a when the
+ * residual is all zero); accept_mask (batch, k) uint8 per-candidate tests.
+ * u_j and the bonus race noise come from Philox4x32-10 (streams 1 and 2 of
+ * the counter's last word), so a call is a pure function of its inputs.
+ * Three launches (row statistics, acceptance + residual race, merge); k <= 32.
+ */
+int sd_verify_batch(const void* draft, int64_t draft_stride_b, int64_t draft_stride_k,
+                    int32_t draft_dtype, const void* target, int64_t target_stride_b,
+                    int64_t target_stride_k, int32_t target_dtype, const int64_t* draft_tokens,
+                    int64_t tokens_stride_b, const float* temperatures,
+                    int32_t draft_is_point_mass, const int64_t* rng_state, int64_t batch,
+                    int32_t k, int32_t vocab, int64_t* accepted, int64_t* bonus,
+                    uint8_t* accept_mask, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,8 @@ holding bf16 numbers; ``bf16.round_f32`` is every conversion back to bf16.
   silu_mul                nanovllm/layers/activation.py:6-11
   philox4x32_10, sample   nanovllm/layers/sampler.py:6-12 (exponential race),
                           with this build's counter-based noise
+  verify_batch            nanovllm/spec_decode/verify.py:39-183 (rejection
+                          sampling), with the same noise
 """
 import numpy as np
 
@@ -137,3 +139,65 @@ def sample(logits, temperatures, seed, offset):
     keys = sample_keys(logits, np.where(temperatures > 0, temperatures, 1), seed, offset)
     greedy = argmax_first(logits)
     return np.where(temperatures > 0, np.argmax(keys, axis=-1), greedy).astype(np.int64)
+
+
+def _philox_word0(c0, c1, c2, c3, seed):
+    return philox4x32_10(c0, c1, c2, c3, np.uint32(seed & 0xFFFFFFFF),
+                         np.uint32((seed >> 32) & 0xFFFFFFFF))[0]
+
+
+def _softmax_rows(x):
+    x = np.asarray(x, dtype=np.float32)
+    m = x.max(axis=-1, keepdims=True)
+    e = np.exp((x - m).astype(np.float32), dtype=np.float32)
+    return (e / e.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
+
+
+def verify_batch(draft, target, tokens, temperatures=None, point_mass=False, seed=0, offset=0):
+    """spec_decode/verify.py:39-183 with this build's noise. Returns
+    (accepted (B,), bonus (B,), accept_mask (B, k)).
+
+    q = softmax(draft / T) (draft as given when point_mass), p = softmax(target / T);
+    candidate j passes when u_j < min(1, p_j[x_j] / max(q_j[x_j], 1e-10)) (never
+    when q_j[x_j] == 0), u_j = (Philox(j, b ^ off_hi, off_lo, 1).c0 >> 8) 2^-24;
+    accepted = first failure (k if none); bonus = argmax(max(0, p_a - q_a) / E)
+    with q_k = 0, or argmax(p_a / E) when that residual is all zero,
+    E_i = max(-log U_i, 1e-10), U_i = ((Philox(i, b ^ off_hi, off_lo, 2).c0 >> 8) + 1) 2^-24.
+    """
+    draft = np.asarray(draft, dtype=np.float32)
+    target = np.asarray(target, dtype=np.float32)
+    B, k, V = draft.shape
+    T = np.ones(B, np.float32) if temperatures is None else np.asarray(temperatures, np.float32)
+    T = np.where(T > 0, T, np.float32(1)).astype(np.float32)
+    q = draft if point_mass else _softmax_rows(draft / T[:, None, None])
+    p = _softmax_rows(target / T[:, None, None])
+    off_lo = np.uint32(offset & 0xFFFFFFFF)
+    off_hi = np.uint32((offset >> 32) & 0xFFFFFFFF)
+    bb = np.arange(B, dtype=np.uint32) ^ off_hi                        # (B,)
+    tok = np.asarray(tokens, dtype=np.int64).reshape(B, k)
+    valid = (tok >= 0) & (tok < V)
+    tc = np.where(valid, tok, 0)
+    qt = np.where(valid, np.take_along_axis(q, tc[:, :, None], 2)[:, :, 0], np.float32(0))
+    pt = np.where(valid, np.take_along_axis(p[:, :k], tc[:, :, None], 2)[:, :, 0], np.float32(0))
+    ratio = np.where(qt > 0, np.minimum(pt / np.maximum(qt, np.float32(1e-10)), np.float32(1)),
+                     np.float32(0)).astype(np.float32)
+    jj = np.broadcast_to(np.arange(k, dtype=np.uint32)[None, :], (B, k))
+    w = _philox_word0(jj, np.broadcast_to(bb[:, None], (B, k)), np.full((B, k), off_lo, np.uint32),
+                      np.ones((B, k), np.uint32), seed)
+    u = (w >> np.uint32(8)).astype(np.float32) * np.float32(1.0 / 16777216.0)
+    mask = u < ratio
+    fail = ~mask
+    accepted = np.where(fail.any(axis=1), fail.argmax(axis=1), k).astype(np.int64)
+    rows = np.arange(B)
+    pa = p[rows, accepted]                                             # (B, V)
+    qpad = np.concatenate([q, np.zeros((B, 1, V), np.float32)], axis=1)
+    qa = qpad[rows, accepted]
+    r = np.maximum(pa - qa, np.float32(0))
+    cols = np.broadcast_to(np.arange(V, dtype=np.uint32)[None, :], (B, V))
+    w2 = _philox_word0(cols, np.broadcast_to(bb[:, None], (B, V)), np.full((B, V), off_lo, np.uint32),
+                       np.full((B, V), 2, np.uint32), seed)
+    U = ((w2 >> np.uint32(8)).astype(np.float32) + np.float32(1)) * np.float32(1.0 / 16777216.0)
+    E = np.maximum(-np.log(U), np.float32(1e-10)).astype(np.float32)
+    use_r = r.sum(axis=1, dtype=np.float32) > 0
+    bonus = np.where(use_r, np.argmax(r / E, axis=1), np.argmax(pa / E, axis=1)).astype(np.int64)
+    return accepted, bonus, mask

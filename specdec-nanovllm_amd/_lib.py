@@ -71,6 +71,14 @@ SIGNATURES.update({
     "sd_sample": (ctypes.c_int, [
         _p, _i64, _i32, _i64, _i32,     # logits, stride, dtype, rows, vocab
         _p, _p, _p, _p]),               # temperatures, rng_state, out_tokens, stream
+    "sd_verify_batch_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "sd_verify_batch": (ctypes.c_int, [
+        _p, _i64, _i64, _i32,           # draft, strides (b, k), dtype
+        _p, _i64, _i64, _i32,           # target, strides, dtype
+        _p, _i64, _p, _i32, _p,         # tokens, stride, temperatures, point_mass, rng_state
+        _i64, _i32, _i32,               # batch, k, vocab
+        _p, _p, _p,                     # accepted, bonus, accept_mask
+        _p, _sz, _p]),                  # workspace, bytes, stream
 })
 SIGNATURES["sd_paged_attention_partial"] = SIGNATURES["sd_paged_attention"]
 SIGNATURES["sd_paged_attention_store"] = (ctypes.c_int, [

@@ -202,28 +202,6 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(SiluParams p) {
 }
 
 // ------------------------------------------------------------------ sampling
-// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
-// as 1, 2, 3", SC 2011): counter (c0..c3), key (k0, k1), ten rounds.
-__device__ __forceinline__ void philox(uint32_t c[4], uint32_t k0, uint32_t k1) {
-  constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
-  constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    const uint64_t p0 = static_cast<uint64_t>(M0) * c[0];
-    const uint64_t p1 = static_cast<uint64_t>(M1) * c[2];
-    const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c[1] ^ k0;
-    const uint32_t n1 = static_cast<uint32_t>(p1);
-    const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c[3] ^ k1;
-    const uint32_t n3 = static_cast<uint32_t>(p0);
-    c[0] = n0;
-    c[1] = n1;
-    c[2] = n2;
-    c[3] = n3;
-    k0 += W0;
-    k1 += W1;
-  }
-}
-
 struct SampleParams {
   const void* logits;
   int64_t ls;
@@ -275,7 +253,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) 
     float key = logit_at(p, row, i);
     if (!greedy) {
       uint32_t c[4] = {static_cast<uint32_t>(i), static_cast<uint32_t>(row) ^ off1, off0, 0u};
-      philox(c, k0, k1);
+      sd::philox(c, k0, k1);
       const float u = (static_cast<float>(c[0] >> 8) + 1.f) * (1.f / 16777216.f);  // (0, 1]
       const float e = fmaxf(-logf(u), 1e-10f);
       key = key * inv_t - logf(e);

@@ -309,20 +309,39 @@ def silu_mul(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     return o.view(*x.shape[:-1], W // 2)
 
 
+# Philox (seed, offset) per device for calls that bring no rng_state: seeded
+# from torch's initial seed, its offset advanced on the stream after each draw
+# (so graph replays draw fresh noise too).
+_RNG_STATES: dict = {}
+
+
+def default_rng_state(dev: torch.device) -> torch.Tensor:
+    st = _RNG_STATES.get(dev.index)
+    if st is None:
+        st = torch.tensor([torch.initial_seed() & 0x7FFFFFFFFFFFFFFF, 0], dtype=torch.int64,
+                          device=dev)
+        _RNG_STATES[dev.index] = st
+    return st
+
+
 def sample(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
            rng_state: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """One token per row of logits (rows, vocab): greedy argmax when
     ``temperatures`` is None (or a row's temperature is <= 0), otherwise the
     exponential-race draw of ``Sampler.forward`` (nanovllm/layers/sampler.py:6-12)
     with Philox noise keyed by ``rng_state`` = (seed, offset) int64 on the device.
-    The caller advances ``rng_state[1]`` between draws."""
+    A given ``rng_state`` is the caller's to advance; without one the device's
+    default state is used and advanced."""
     assert logits.dim() == 2 and logits.stride(-1) == 1
     rows, V = logits.shape
     t = None
+    advance = False
     if temperatures is not None:
         t = temperatures.reshape(-1).to(torch.float32).contiguous()
-        assert t.numel() == rows and rng_state is not None and rng_state.numel() == 2
-        assert rng_state.dtype == torch.int64
+        assert t.numel() == rows
+        if rng_state is None:
+            rng_state, advance = default_rng_state(logits.device), True
+        assert rng_state.numel() == 2 and rng_state.dtype == torch.int64
     dev = _lib.require_device(logits, t, rng_state, out)
     o = torch.empty(rows, dtype=torch.int64, device=dev) if out is None else out
     assert o.dtype == torch.int64 and o.numel() == rows and o.is_contiguous()
@@ -333,4 +352,55 @@ def sample(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
                                rows, V, _ptr(t), _ptr(rng_state), o.data_ptr(),
                                _lib.stream_ptr(dev))
         _lib.check(rc)
+        if advance:
+            rng_state[1:].add_(1)
     return o
+
+
+def verify_batch(draft: torch.Tensor, target_logits: torch.Tensor, draft_tokens: torch.Tensor,
+                 temperatures: torch.Tensor | None = None, draft_is_point_mass: bool = False,
+                 rng_state: torch.Tensor | None = None):
+    """Rejection-sampling verification (nanovllm/spec_decode/verify.py:39-183):
+    returns (accepted (B,) int64, bonus (B,) int64, accept_mask (B, k) bool).
+
+    ``draft`` (B, k, V): the draft's raw logits, or its probabilities with
+    ``draft_is_point_mass``; ``target_logits`` (B, k + 1, V); the row dims may
+    be strided, the vocabulary contiguous. Noise is Philox keyed by
+    ``rng_state`` (seed, offset) on the device; without one the device's
+    default state is used and advanced."""
+    assert draft.dim() == 3 and target_logits.dim() == 3 and draft_tokens.dim() == 2
+    B, k, V = draft.shape
+    assert target_logits.shape[0] == B and target_logits.shape[2] == V
+    assert target_logits.shape[1] == k + 1, "target_logits must hold k + 1 rows"
+    assert draft_tokens.shape == (B, k)
+    assert draft.stride(-1) == 1 and target_logits.stride(-1) == 1
+    tok = draft_tokens if draft_tokens.dtype == torch.int64 else draft_tokens.to(torch.int64)
+    if tok.stride(-1) != 1:
+        tok = tok.contiguous()
+    t = None if temperatures is None else temperatures.reshape(-1).to(torch.float32).contiguous()
+    if t is not None and t.numel() == 1 and B > 1:
+        t = t.expand(B).contiguous()
+    advance = rng_state is None
+    if advance:
+        rng_state = default_rng_state(draft.device)
+    dev = _lib.require_device(draft, target_logits, tok, t, rng_state)
+    accepted = torch.empty(B, dtype=torch.int64, device=dev)
+    bonus = torch.empty(B, dtype=torch.int64, device=dev)
+    mask = torch.empty((B, k), dtype=torch.bool, device=dev)
+    if B:
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            ws_bytes = lib.sd_verify_batch_workspace_size(B, k, V)
+            ws = _workspace(ws_bytes, dev)
+            rc = lib.sd_verify_batch(draft.data_ptr(), draft.stride(0), draft.stride(1),
+                                     _lib.dtype_code(draft.dtype), target_logits.data_ptr(),
+                                     target_logits.stride(0), target_logits.stride(1),
+                                     _lib.dtype_code(target_logits.dtype), tok.data_ptr(),
+                                     tok.stride(0), _ptr(t), int(bool(draft_is_point_mass)),
+                                     rng_state.data_ptr(), B, k, V, accepted.data_ptr(),
+                                     bonus.data_ptr(), mask.data_ptr(), _ptr(ws), ws_bytes,
+                                     _lib.stream_ptr(dev))
+        _lib.check(rc)
+        if advance:
+            rng_state[1:].add_(1)
+    return accepted, bonus, mask
