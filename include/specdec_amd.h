@@ -200,6 +200,20 @@ int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t 
                     int64_t K, int32_t dtype, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/*
+ * Symmetric int8 weight quantization, the producer of the W8A16 format:
+ * `quantize_weight` (nanovllm/layers/quant.py:123-148) and the offline
+ * converter's `quantize_tensor` (scripts/quantize_int8.py:53-83). Per row and
+ * group (group_size columns, or the whole row when group_size == 0), in fp32:
+ * scale = max(max|w| / 127, 1e-8); q = clamp(round_half_even(w / scale), -127,
+ * 127). Writes q (N, K) int8 (row stride q_stride) and scale (N, K / group)
+ * bf16 row-major (the fp32 scale rounded to nearest even, after q).
+ *   w: (N, K) bf16/f16/f32, 16-byte aligned rows; K and the group size
+ *   multiples of 8, the group size dividing K.
+ */
+int sd_quantize_int8(const void* w, int64_t w_stride, int32_t dtype, int8_t* q, int64_t q_stride,
+                     void* scale, int64_t N, int32_t K, int32_t group_size, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Neighbours of the draft step (the row-wise work of a Qwen3 decoder step
  * between the attention and linear launches). Eager-torch rounding: fp32

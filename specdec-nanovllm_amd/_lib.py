@@ -71,6 +71,9 @@ SIGNATURES.update({
     "sd_sample": (ctypes.c_int, [
         _p, _i64, _i32, _i64, _i32,     # logits, stride, dtype, rows, vocab
         _p, _p, _p, _p]),               # temperatures, rng_state, out_tokens, stream
+    "sd_quantize_int8": (ctypes.c_int, [
+        _p, _i64, _i32, _p, _i64,       # w, stride, dtype, q, stride
+        _p, _i64, _i32, _i32, _p]),     # scale, N, K, group_size, stream
     "sd_verify_batch_workspace_size": (_sz, [_i64, _i32, _i32]),
     "sd_verify_batch": (ctypes.c_int, [
         _p, _i64, _i64, _i32,           # draft, strides (b, k), dtype

@@ -5,13 +5,18 @@
   floats only in registers; fp32 accumulation; the per-channel scale
   multiplies the fp32 accumulator. The output dtype is the activation dtype
   (the reference always writes bf16, and only ever receives bf16).
-* ``quantize_weight`` / ``dequantize_weight`` — the symmetric quantizer and the
-  reference dequantization (quant.py:123-159), plain torch on whatever device
-  the weight lives on; they run at load time, not on the decode path.
+* ``quantize_weight`` — the symmetric quantizer (quant.py:123-148) on the gfx950
+  quantize kernel (bit-identical to the reference's fp32 formula; a weight on
+  the CPU is an error, as for every op here); ``dequantize_weight`` — the
+  reference dequantization (quant.py:151-159) in plain torch, for checking.
+* ``hf_names_to_modules`` — checkpoint tensor names to engine module names
+  (quant.py:31-63).
 * ``apply_int8_quant`` — in-place swap of named linear layers to int8
   (quant.py:66-117).
 """
 from __future__ import annotations
+
+import re
 
 import torch
 import torch.nn as nn
@@ -31,18 +36,43 @@ def quantize_weight(w: torch.Tensor, granularity: str = "per_channel", group_siz
     """
     assert w.dim() == 2, f"expects a 2-D weight, got {tuple(w.shape)}"
     N, K = w.shape
-    wf = w.to(torch.float32)
     if granularity == "per_channel":
-        grouped = wf.view(N, 1, K)
-    elif granularity == "per_group":
+        q, scale = ops.quantize_int8(w, 0)
+        return q, scale.view(N)
+    if granularity == "per_group":
         assert group_size > 0 and K % group_size == 0
-        grouped = wf.view(N, K // group_size, group_size)
-    else:
-        raise ValueError(granularity)
-    scale = (grouped.abs().amax(dim=2, keepdim=True) / QMAX).clamp_min(1e-8)
-    q = torch.round(grouped / scale).clamp(-QMAX, QMAX).to(torch.int8).view(N, K)
-    scale = scale.view(N) if granularity == "per_channel" else scale.view(N, K // group_size)
-    return q.contiguous(), scale.to(torch.bfloat16).contiguous()
+        return ops.quantize_int8(w, group_size)
+    raise ValueError(granularity)
+
+
+# Checkpoint (HF) tensor names -> engine module names: q/k/v are one qkv_proj
+# and gate/up one gate_up_proj in the engine (quant.py:31-38).
+_HF_TO_ENGINE = [
+    (re.compile(r"^(.*)\.self_attn\.(?:q|k|v)_proj\.weight$"), r"\1.self_attn.qkv_proj"),
+    (re.compile(r"^(.*)\.self_attn\.o_proj\.weight$"), r"\1.self_attn.o_proj"),
+    (re.compile(r"^(.*)\.mlp\.(?:gate|up)_proj\.weight$"), r"\1.mlp.gate_up_proj"),
+    (re.compile(r"^(.*)\.mlp\.down_proj\.weight$"), r"\1.mlp.down_proj"),
+]
+
+
+def hf_names_to_modules(hf_names):
+    """quant.py:41-63: the engine modules a quant_config's ``quantized_layers``
+    name. A packed module must be complete (q, k and v; gate and up), else
+    ValueError — never a half-quantized module."""
+    groups = {}
+    for n in hf_names:
+        for rx, rep in _HF_TO_ENGINE:
+            if rx.match(n):
+                groups.setdefault(rx.sub(rep, n), set()).add(n)
+                break
+        else:
+            raise ValueError(f"unrecognised quantized layer name: {n}")
+    for mod, src in groups.items():
+        if mod.endswith("qkv_proj") and len(src) != 3:
+            raise ValueError(f"{mod} needs q, k and v together, got {sorted(src)}")
+        if mod.endswith("gate_up_proj") and len(src) != 2:
+            raise ValueError(f"{mod} needs gate and up together, got {sorted(src)}")
+    return sorted(groups)
 
 
 def dequantize_weight(q: torch.Tensor, scale: torch.Tensor,

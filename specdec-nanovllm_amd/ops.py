@@ -215,6 +215,31 @@ def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
     return y.view(*x.shape[:-1], N)
 
 
+def quantize_int8(w: torch.Tensor, group_size: int = 0):
+    """Symmetric int8 quantization of a 2-D weight on the GPU (the W8A16
+    format's producer, nanovllm/layers/quant.py:123-148): per row (group_size
+    0) or per group of columns, scale = max(max|w| / 127, 1e-8) in fp32,
+    q = clamp(round_half_even(w / scale), -127, 127). Returns (q int8 (N, K),
+    scale bf16 (N, K // group) — the fp32 scale rounded after q)."""
+    assert w.dim() == 2, f"expects a 2-D weight, got {tuple(w.shape)}"
+    N, K = w.shape
+    G = group_size if group_size > 0 else K
+    assert K % G == 0, "group_size must divide K"
+    if w.stride(-1) != 1 or w.data_ptr() % 16 or (N > 1 and w.stride(0) % 8):
+        w = w.contiguous()
+    dev = _lib.require_device(w)
+    q = torch.empty((N, K), dtype=torch.int8, device=dev)
+    scale = torch.empty((N, K // G), dtype=torch.bfloat16, device=dev)
+    if N:
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            rc = lib.sd_quantize_int8(w.data_ptr(), w.stride(0), _lib.dtype_code(w.dtype),
+                                      q.data_ptr(), q.stride(0), scale.data_ptr(), N, K,
+                                      int(group_size), _lib.stream_ptr(dev))
+        _lib.check(rc)
+    return q, scale
+
+
 # --------------------------------------------------------------- draft-step neighbours
 def _rows16(t: torch.Tensor, what: str) -> torch.Tensor:
     """2-D (rows, width) view with a unit last stride and 16-byte aligned rows."""
