@@ -177,3 +177,29 @@ def test_sampling_law_on_gpu():
     counts = np.bincount(toks, minlength=V)
     chi2 = (((counts - rows * p) ** 2) / (rows * p)).sum()
     assert chi2 < 20.5
+
+
+# ------------------------------------------------------- reference-named modules
+def test_reference_named_modules():
+    from specdec_nanovllm_amd.layers.activation import SiluAndMul
+    from specdec_nanovllm_amd.layers.layernorm import RMSNorm
+    from specdec_nanovllm_amd.layers.rotary_embedding import get_rope
+    x = rand((5, 1024), 31, torch.bfloat16).to(DEV)
+    r = rand((5, 1024), 32, torch.bfloat16).to(DEV)
+    norm = RMSNorm(1024).to(DEV).to(torch.bfloat16)
+    assert torch.equal(norm(x), ops.rmsnorm(x, norm.weight, 1e-6))
+    o, res = norm(x, r)
+    o2, res2 = ops.rmsnorm(x, norm.weight, 1e-6, residual=r)
+    assert torch.equal(o, o2) and torch.equal(res, res2)
+    gu = rand((3, 2 * 512), 33, torch.bfloat16).to(DEV)
+    assert torch.equal(SiluAndMul()(gu), ops.silu_mul(gu))
+    rope = get_rope(128, 128, 4096, 1e6).to(DEV)
+    q = rand((4, 16 * 128), 34, torch.bfloat16).to(DEV)
+    k = rand((4, 8 * 128), 35, torch.bfloat16).to(DEV)
+    pos = torch.tensor([0, 5, 100, 4095], device=DEV)
+    q2, k2 = rope(pos, q, k)
+    assert q2.shape == q.shape and torch.equal(q2.view(4, 16, 128)[0], q.view(4, 16, 128)[0])
+    rq, rk = od.qk_norm_rope(to_np(q.float()).reshape(4, 16, 128), to_np(k.float()).reshape(4, 8, 128),
+                             pos.cpu().numpy(), rope.cos_sin_cache.view(4096, 128).cpu().numpy())
+    assert_units(to_np(q2.float()).reshape(4, 16, 128), rq, "rope q", units=4, per_row=True)
+    assert_units(to_np(k2.float()).reshape(4, 8, 128), rk, "rope k", units=4, per_row=True)
