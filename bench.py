@@ -245,6 +245,26 @@ def bench_verify_batch(ops, torch, steps):
             "GBps": round(nbytes / ms / 1e6, 1), "bytes": nbytes}
 
 
+def bench_prefill(ops, torch, steps):
+    """Prefill attention (flash_attn_varlen_func's causal varlen form): B = 4
+    sequences of 2048 tokens, Qwen3-4B attention 32q/8kv/128, bf16, contiguous
+    K/V. FLOPs: 4 D Hq per visible (query, key) pair, sum over t of (t + 1) keys."""
+    B, L, hq, hkv = 4, 2048, 32, 8
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    q = torch.randn((B * L, hq, 128), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((B * L, hkv, 128), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((B * L, hkv, 128), generator=g, device="cuda").to(torch.bfloat16)
+    cu = torch.arange(0, (B + 1) * L, L, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    g_ = graph_of(lambda: ops.prefill_attention(q, k, v, cu, cu, L, 128 ** -0.5, out=out), torch)
+    ms = time_replays([g_], steps, 3, torch)
+    flops = 4 * 128 * hq * B * (L * (L + 1) // 2)
+    return {"config": "prefill B=4 x 2048 tokens, 32q/8kv/128 bf16, causal", "us": round(ms * 1e3, 2),
+            "TFLOPs": round(flops / ms / 1e9, 1),
+            "frac_of_bf16_peak": round(flops / ms / 1e9 / 2500.0, 4)}
+
+
 def bench_draft_chain(workloads_mod, torch, reps=5):
     """C5: hipGraph-captured k = 6 greedy draft steps of a random-init
     Qwen3-0.6B (28 layers, all linears W8A16, paged bf16 KV with a 2048-token
@@ -415,6 +435,8 @@ def main():
         extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100))
         torch.cuda.empty_cache()
         extra["verify_batch"] = bench_verify_batch(ops, torch, min(args.steps, 100))
+        torch.cuda.empty_cache()
+        extra["prefill"] = bench_prefill(ops, torch, min(args.steps, 50))
         torch.cuda.empty_cache()
         if not args.no_draft_chain:
             extra["draft_chain"] = bench_draft_chain(workloads, torch)

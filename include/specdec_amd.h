@@ -279,6 +279,33 @@ int sd_sample(const void* logits, int64_t logits_stride, int32_t dtype, int64_t 
               int64_t* out_tokens, void* stream);
 
 /*
+ * Variable-length causal attention, the prefill branch of the attention layer:
+ * flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+ * max_seqlen_k, softmax_scale, causal=True, block_table)
+ * (nanovllm/layers/attention.py:64-70). Query row t of sequence b attends keys
+ * [0, nk_b - nq_b + t] (bottom-right aligned), nq_b / nk_b from the cu arrays.
+ *   q   : (total_q, num_q_heads, 128), row strides as given
+ *   k/v : block_table == NULL: contiguous (total_k, num_kv_heads, 128) with
+ *         kv_stride_tok / kv_stride_head (kv_stride_block unused), rows of
+ *         sequence b from cu_seqlens_k[b];
+ *         block_table != NULL: the paged cache, (num_blocks, block_size,
+ *         num_kv_heads, 128) by kv_stride_block / kv_stride_tok /
+ *         kv_stride_head (the prefix-cache case)
+ *   out : (total_q, num_q_heads, 128)
+ * head_dim 128, num_q_heads / num_kv_heads dividing 64, bf16/f16; 16-byte
+ * aligned rows. One launch, no workspace.
+ */
+int sd_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                         const void* k, const void* v, int64_t kv_stride_tok,
+                         int64_t kv_stride_head, int64_t kv_stride_block, int64_t num_blocks,
+                         int32_t block_size, const int32_t* block_table, int64_t bt_stride,
+                         int32_t max_blocks_per_seq, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, int32_t max_seqlen_q, int64_t total_q,
+                         int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                         int32_t head_dim, float scale, int32_t dtype, void* out,
+                         int64_t out_stride_tok, int64_t out_stride_head, void* stream);
+
+/*
  * Workspace bytes of sd_verify_batch (0 for an empty batch).
  */
 size_t sd_verify_batch_workspace_size(int64_t batch, int32_t k, int32_t vocab);

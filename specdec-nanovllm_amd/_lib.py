@@ -74,6 +74,13 @@ SIGNATURES.update({
     "sd_quantize_int8": (ctypes.c_int, [
         _p, _i64, _i32, _p, _i64,       # w, stride, dtype, q, stride
         _p, _i64, _i32, _i32, _p]),     # scale, N, K, group_size, stream
+    "sd_prefill_attention": (ctypes.c_int, [
+        _p, _i64, _i64, _p, _p,         # q, strides (tok, head), k, v
+        _i64, _i64, _i64, _i64, _i32,   # kv strides (tok, head, block), num_blocks, block_size
+        _p, _i64, _i32,                 # block_table, bt_stride, max_blocks
+        _p, _p, _i32, _i64, _i32,       # cu_q, cu_k, max_seqlen_q, total_q, num_seqs
+        _i32, _i32, _i32, _f32, _i32,   # hq, hkv, head_dim, scale, dtype
+        _p, _i64, _i64, _p]),           # out, strides, stream
     "sd_verify_batch_workspace_size": (_sz, [_i64, _i32, _i32]),
     "sd_verify_batch": (ctypes.c_int, [
         _p, _i64, _i64, _i32,           # draft, strides (b, k), dtype

@@ -9,9 +9,13 @@ the paged cases on the decode hot path and served by the gfx950 kernel.
   ``cu_seqlens_k[b+1] - cu_seqlens_k[b]`` keys, bottom-right causal), as set
   up by ``prepare_verify`` (nanovllm/engine/model_runner.py:492-584).
 
-Supported: paged KV (``block_table`` given), head_dim 128, (Hq / Hkv) * q rows
-per sequence <= 32. Contiguous-KV prefill is outside this library and raises
-``NotImplementedError``.
+* ``flash_attn_varlen_func`` without ``block_table`` (or with one and many
+  rows per sequence) — the prefill call at attention.py:64-70, contiguous K/V
+  (or the prefix-cached pages), served by the prefill kernel.
+
+Supported: head_dim 128; causal (bottom-right) whenever a sequence has several
+query rows. The decode kernel takes (Hq / Hkv) * q rows per sequence <= 32 (decode
+and verify); longer query blocks go to the prefill kernel.
 """
 from __future__ import annotations
 
@@ -50,14 +54,15 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
                            dropout_p=0.0, softmax_scale=None, causal=False, block_table=None,
                            **unused):
     """Variable-length attention of ``q`` (total_q, Hq, D); ``k``/``v`` are the
-    paged caches when ``block_table`` is given. Returns (total_q, Hq, D)."""
-    if block_table is None:
-        raise NotImplementedError("contiguous-KV (prefill) varlen attention is not part of "
-                                  "this library; pass the paged cache and block_table")
+    paged caches when ``block_table`` is given, contiguous (total_k, Hkv, D)
+    rows otherwise. Returns (total_q, Hq, D)."""
     if dropout_p:
         raise NotImplementedError("dropout")
     if int(max_seqlen_q) > 1 and not causal:
         raise NotImplementedError("non-causal attention with several query rows")
     scale = softmax_scale if softmax_scale is not None else q.shape[-1] ** -0.5
-    return ops.paged_attention(q, k, v, block_table, scale, cu_seqlens_k=cu_seqlens_k,
-                               cu_seqlens_q=cu_seqlens_q, max_seqlen_q=int(max_seqlen_q))
+    if block_table is not None and (q.shape[1] // k.shape[2]) * int(max_seqlen_q) <= 32:
+        return ops.paged_attention(q, k, v, block_table, scale, cu_seqlens_k=cu_seqlens_k,
+                                   cu_seqlens_q=cu_seqlens_q, max_seqlen_q=int(max_seqlen_q))
+    return ops.prefill_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), scale,
+                                 block_table=block_table)

@@ -42,18 +42,28 @@ class Attention(nn.Module):
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
         has_cache = bool(k_cache.numel() and v_cache.numel())
-        if context.is_prefill and context.block_tables is None:
-            raise NotImplementedError("prefill over contiguous k/v is outside the decode "
-                                      "hot path served by this library")
+        if context.is_prefill:  # attention.py:62-70
+            G = self.num_heads // self.num_kv_heads
+            if (has_cache and context.block_tables is not None
+                    and G * int(context.max_seqlen_q) <= 32):
+                # speculative verify / short prefix-cache rows: store_kvcache of k / v
+                # and the paged attention in one call
+                return ops.paged_attention(q, k_cache, v_cache, context.block_tables,
+                                           self.scale, cu_seqlens_k=context.cu_seqlens_k,
+                                           cu_seqlens_q=context.cu_seqlens_q,
+                                           max_seqlen_q=int(context.max_seqlen_q),
+                                           key=k, value=v, slot_mapping=context.slot_mapping)
+            if has_cache:
+                store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
+            if context.block_tables is not None:  # prefix cache: keys come from the pages
+                if not has_cache:
+                    raise RuntimeError("prefix-cached prefill needs the paged k_cache / v_cache")
+                k, v = k_cache, v_cache
+            return ops.prefill_attention(q, k, v, context.cu_seqlens_q, context.cu_seqlens_k,
+                                         int(context.max_seqlen_q), self.scale,
+                                         block_table=context.block_tables)
         if not has_cache:
             raise RuntimeError("Attention needs its paged k_cache / v_cache")
-        # store_kvcache of k / v and the paged attention in one launch
-        if context.is_prefill:  # speculative verify / prefix-cache rows (attention.py:64-70)
-            return ops.paged_attention(q, k_cache, v_cache, context.block_tables, self.scale,
-                                       cu_seqlens_k=context.cu_seqlens_k,
-                                       cu_seqlens_q=context.cu_seqlens_q,
-                                       max_seqlen_q=int(context.max_seqlen_q),
-                                       key=k, value=v, slot_mapping=context.slot_mapping)
         # decode (attention.py:71-81): q is (B, Hq, D), or (Hq, D) for one sequence;
         # the result has flash_attn_with_kvcache's (B, 1, Hq, D) shape
         if q.dim() == 2:

@@ -170,6 +170,51 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     return out
 
 
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                      max_seqlen_q: int, scale: float, block_table: torch.Tensor | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Variable-length causal attention (the prefill call of the attention layer,
+    nanovllm/layers/attention.py:64-70): q (total_q, Hq, 128); ``k``/``v`` are
+    contiguous (total_k, Hkv, 128) rows when ``block_table`` is None, else the
+    paged caches (num_blocks, block_size, Hkv, 128). Row t of sequence b sees
+    keys [0, nk_b - nq_b + t]. Returns (total_q, Hq, 128)."""
+    total_q, num_q_heads, head_dim = q.shape
+    assert k.shape == v.shape and k.stride() == v.stride()
+    assert q.stride(-1) == 1 and k.stride(-1) == 1
+    num_seqs = cu_seqlens_q.numel() - 1
+    cuq, cuk = _i32(cu_seqlens_q), _i32(cu_seqlens_k)
+    assert cuk.numel() == num_seqs + 1
+    if block_table is None:
+        assert k.dim() == 3, "contiguous k/v must be (total_k, Hkv, D)"
+        num_kv_heads = k.shape[1]
+        s_tok, s_head, s_blk, num_blocks, block_size = k.stride(0), k.stride(1), 0, 0, 0
+        bt, bt_stride, max_blocks = None, 0, 0
+    else:
+        assert k.dim() == 4, "paged k/v cache must be (num_blocks, block_size, Hkv, D)"
+        num_blocks, block_size, num_kv_heads, _ = k.shape
+        s_blk, s_tok, s_head = k.stride(0), k.stride(1), k.stride(2)
+        bt = _i32(block_table)
+        bt_stride, max_blocks = bt.stride(0), bt.shape[1]
+    assert num_q_heads % num_kv_heads == 0, "GQA needs num_q_heads % num_kv_heads == 0"
+    dev = _lib.require_device(q, k, v, cuq, cuk, bt, out)
+    if out is None:
+        out = torch.empty_like(q)
+    if num_seqs <= 0 or total_q == 0:
+        return out
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.sd_prefill_attention(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                                      v.data_ptr(), s_tok, s_head, s_blk, num_blocks, block_size,
+                                      _ptr(bt), bt_stride, max_blocks, cuq.data_ptr(),
+                                      cuk.data_ptr(), int(max_seqlen_q), total_q, num_seqs,
+                                      num_q_heads, num_kv_heads, head_dim, float(scale),
+                                      _lib.dtype_code(q.dtype), out.data_ptr(), out.stride(0),
+                                      out.stride(1), _lib.stream_ptr(dev))
+    _lib.check(rc)
+    return out
+
+
 # -------------------------------------------------------------------------- w8a16
 def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
                  bias: torch.Tensor | None = None, group_size: int = 0,
