@@ -148,14 +148,15 @@ int sd_paged_attention_partial(const void* q, int64_t q_stride_tok, int64_t q_st
  * Arguments as sd_paged_attention, plus the new rows: key/value
  * (total_q, num_kv_heads, head_dim) and slot_mapping (total_q,), row t being
  * query row t's key/value (decode: one per sequence; verify: the n_b rows of
- * sequence b). Result: bit for bit the same cache as sd_store_kvcache and the
- * same output as sd_paged_attention afterwards, PROVIDED that the new rows of
- * sequence b are its last n_b keys in block_table order with slot -1 or the
- * slot of that position — what prepare_decode / prepare_verify and the draft
- * proposer produce (model_runner.py:466-482,522-548, draft_proposer.py:527-550).
- * The attention kernel reads the new rows straight from key/value and the
- * copies into the cache ride in the second (combine) launch, so no kernel
- * waits for the store. num_seqs == 0 with total_q > 0 only stores.
+ * sequence b). Result: bit for bit the same cache as sd_store_kvcache, and the
+ * output of sd_paged_attention afterwards up to rounding (within the attention
+ * tolerance), PROVIDED that the new rows of sequence b are its last n_b keys in
+ * block_table order with slot -1 or the slot of that position — what
+ * prepare_decode / prepare_verify and the draft proposer produce
+ * (model_runner.py:466-482,522-548, draft_proposer.py:527-550). The main
+ * kernel attends over the cached keys; the second (combine) launch adds the
+ * new keys from key/value (fp32 scores) and copies the rows into the cache, so
+ * no kernel waits for the store. num_seqs == 0 with total_q > 0 only stores.
  */
 int sd_paged_attention_store(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
                              const void* value, int64_t value_stride_tok,

@@ -8,14 +8,19 @@
 // rule of the verify forward (nanovllm/layers/attention.py:64-70,
 // nanovllm/engine/model_runner.py:522-533).
 //
-// Work decomposition (stream-K over keys):
-//   A "pair" is one (sequence b, kv head h); it has ceil(L_b / 128) workgroup
-//   steps of 128 keys. All pairs' steps are laid end to end (b major, h
-//   minor) and the grid's `nwg` workgroups each take one contiguous run of
-//   S = max(ceil(T / nwg), min_steps) steps, so every workgroup streams the
+// Work decomposition (stream-K over keys, in columns):
+//   A "pair" is one (sequence b, kv head h); a "column" is 128 keys of one
+//   sequence (all kv heads), so sequence b has ceil(L_b / 128) columns. All
+//   columns are laid end to end (b major) and cut into R = nwg / Hkv runs of
+//   S = max(ceil(C / R), min_steps) columns; workgroup w takes head w % Hkv of
+//   run w / Hkv, one workgroup step per column. Every workgroup streams the
 //   same number of bytes whatever the length mix, with no host sync: each
-//   workgroup derives T and its start from context_lens itself (a wave-wide
-//   scan of the B lengths).
+//   workgroup derives C and its start from context_lens itself (a wave-wide
+//   scan of the B lengths). The Hkv workgroups of a run are dispatched
+//   together and read the same key rows of their Hkv heads at the same time,
+//   so each stretch of a page (key rows of all heads side by side) is
+//   fetched from HBM by one burst of neighbouring requests instead of Hkv
+//   visits at unrelated times.
 //   step  : the 4 wave64s of a workgroup take 32 keys each. A wave loads the
 //           next step's K and V rows (16-byte loads) while it computes the
 //           current one (register double buffer), then per 32 keys
@@ -28,11 +33,18 @@
 //   flush : when a pair ends (or the run does) the four waves' (m, l, acc)
 //           meet in LDS. A pair covered by one workgroup is written out
 //           normalised; otherwise the workgroup writes a partial to slot
-//           (workgroup + pair) of the workspace and `paged_attn_combine`
+//           (run + b) * Hkv + h of the workspace and `paged_attn_combine`
 //           merges the partials of each pair (that slot is unique: a later
-//           workgroup can only meet a later pair).
+//           run can only meet a later sequence).
 // G * max_qlen query rows are padded to RT tiles of 16 rows (RT = 1: decode
 // with G <= 16 or the 0.6B verify; RT = 2: Qwen3-4B verify with 7 x 4 rows).
+//
+// Fused store_kvcache (STORE): a sequence's last n_b keys are this launch's new
+// rows. The main kernel walks only the cached keys [0, L_b - n_b), which every
+// query row of the sequence sees, and always writes partials; the combine
+// kernel merges them with the n_b new keys (read from key / value, fp32 dot
+// products, bottom-right causal among the new rows) and copies the new rows
+// to their slots. The hot loop of the store launch is the plain one.
 #include <math.h>
 
 #include "sd_common.h"
@@ -78,8 +90,8 @@ struct AttnParams {
   int64_t o_stok, o_shead;
   float* ws_ml;       // [slots][rmax][2]  (m in log2 units, l)
   float* ws_acc;      // [slots][rmax][kD] unnormalised
-  int32_t nwg;        // workgroups the steps are divided among
-  int32_t min_steps;  // lower bound of steps per workgroup
+  int32_t nwg;        // workgroups: runs * Hkv
+  int32_t min_steps;  // lower bound of columns per run
   int32_t rmax;       // G * max_qlen
   // Fused store_kvcache (knew == NULL: none). Query row t's key/value row is
   // knew/vnew row t; sequence b's rows are its last n_b keys.
@@ -91,10 +103,11 @@ struct AttnParams {
 };
 
 struct SeqInfo {
-  int L;   // keys
-  int nq;  // query rows
+  int L;       // keys the main kernel walks (STORE: cached keys only)
+  int causal;  // row qi sees keys <= causal + qi (and < L)
+  int nq;      // query rows
   int64_t q0;
-  int R;   // G * nq
+  int R;       // G * nq
 };
 
 __device__ __forceinline__ int seq_keys(const AttnParams& p, int b) {
@@ -102,30 +115,38 @@ __device__ __forceinline__ int seq_keys(const AttnParams& p, int b) {
   return min(max(L, 0), p.max_ctx);
 }
 
-// seq_keys for a wave-uniform b (scalar loads).
-__device__ __forceinline__ int seq_keys_uniform(const AttnParams& p, int b) {
-  const int L = p.ctx ? sd::load_scalar_i32(p.ctx + b)
-                      : sd::load_scalar_i32(p.cu_k + b + 1) - sd::load_scalar_i32(p.cu_k + b);
-  return min(max(L, 0), p.max_ctx);
+__device__ __forceinline__ int seq_rows(const AttnParams& p, int b) {
+  return p.cu_q ? min(max(p.cu_q[b + 1] - p.cu_q[b], 0), p.max_qlen) : 1;
+}
+
+// Keys the main kernel walks: all of them, or (STORE) the cached ones.
+template <bool STORE>
+__device__ __forceinline__ int walk_keys(const AttnParams& p, int b) {
+  const int L = seq_keys(p, b);
+  return STORE ? max(L - seq_rows(p, b), 0) : L;
+}
+
+// walk_keys for a wave-uniform b (scalar loads).
+template <bool STORE>
+__device__ __forceinline__ int walk_keys_uniform(const AttnParams& p, int b) {
+  int L = p.ctx ? sd::load_scalar_i32(p.ctx + b)
+                : sd::load_scalar_i32(p.cu_k + b + 1) - sd::load_scalar_i32(p.cu_k + b);
+  L = min(max(L, 0), p.max_ctx);
+  if constexpr (STORE) {
+    const int nq = p.cu_q ? min(max(sd::load_scalar_i32(p.cu_q + b + 1) -
+                                        sd::load_scalar_i32(p.cu_q + b), 0), p.max_qlen)
+                          : 1;
+    L = max(L - nq, 0);
+  }
+  return L;
 }
 
 __device__ __forceinline__ int steps_of(int L) { return (L + kTile - 1) / kTile; }
 
-// First query row and row count of a wave-uniform sequence b (scalar loads).
-__device__ __forceinline__ void seq_rows_uniform(const AttnParams& p, int b, int64_t& q0, int& nq) {
-  if (p.cu_q) {
-    const int a = sd::load_scalar_i32(p.cu_q + b), e = sd::load_scalar_i32(p.cu_q + b + 1);
-    q0 = a;
-    nq = min(max(e - a, 0), p.max_qlen);
-  } else {
-    q0 = b;
-    nq = 1;
-  }
-}
-
+template <bool STORE>
 __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b) {
   SeqInfo s;
-  s.L = seq_keys(p, b);
+  const int L = seq_keys(p, b);
   if (p.cu_q) {
     s.q0 = p.cu_q[b];
     s.nq = min(max(p.cu_q[b + 1] - p.cu_q[b], 0), p.max_qlen);
@@ -133,31 +154,35 @@ __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b) {
     s.q0 = b;
     s.nq = 1;
   }
+  s.L = STORE ? max(L - s.nq, 0) : L;
+  s.causal = L - s.nq;
   s.R = p.G * s.nq;
   return s;
 }
 
-// Wave-wide sum of Hkv * steps(b) over b in [0, upto) (every lane gets it).
-__device__ int steps_before(const AttnParams& p, int upto) {
+// Wave-wide sum of steps(b) (columns) over b in [0, upto) (every lane gets it).
+template <bool STORE>
+__device__ int cols_before(const AttnParams& p, int upto) {
   const int lane = threadIdx.x & 63;
   int sum = 0;
   for (int c = 0; c < upto; c += 64) {
     const int b = c + lane;
-    sum += b < upto ? steps_of(seq_keys(p, b)) : 0;
+    sum += b < upto ? steps_of(walk_keys<STORE>(p, b)) : 0;
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-  return sum * p.Hkv;
+  return sum;
 }
 
-// Wave-wide: the sequence holding global step s (0 <= s < total) and the
-// global index of that sequence's first step.
+// Wave-wide: the sequence holding column s (0 <= s < total) and the index of
+// that sequence's first column.
+template <bool STORE>
 __device__ void locate(const AttnParams& p, int s, int& b_out, int& first_out) {
   const int lane = threadIdx.x & 63;
   int run = 0;
   for (int c = 0; c < p.num_seqs; c += 64) {
     const int b = c + lane;
-    const int n = b < p.num_seqs ? steps_of(seq_keys(p, b)) * p.Hkv : 0;
+    const int n = b < p.num_seqs ? steps_of(walk_keys<STORE>(p, b)) : 0;
     int incl = n;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -180,9 +205,9 @@ __device__ void locate(const AttnParams& p, int s, int& b_out, int& first_out) {
 
 // Fused store: the 16-byte pieces of the new K and V rows, copied to their
 // slots bit for bit (slot -1 or outside the pool: skipped), as store_kvcache
-// does. The main kernel never reads those cache rows (it takes new rows from
-// knew / vnew), so the combine kernel, which runs after it, does the copies:
-// each thread loads its first piece on entry and writes it after its merge.
+// does. The main kernel reads only cached keys, so the combine kernel, which
+// runs after it, does the copies: each thread loads its first piece on entry
+// and writes it after its merge.
 struct StorePiece {
   u32x4 data;
   int64_t slot;
@@ -258,7 +283,6 @@ constexpr int smem_bytes() {
 struct StepRegs {
   u32x4 k[8];
   u32x4 v[8];
-  int slotv;  // fused store, steps holding new rows: slot of new row (lane & 31)
 };
 
 // ONE_PAGE: block_size % 32 == 0, so a wave's 32-key slice never crosses a
@@ -278,22 +302,23 @@ void paged_attn_main(AttnParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
 
-  // ---- this workgroup's run of steps [s0, s1)
-  const int total = __builtin_amdgcn_readfirstlane(steps_before(p, p.num_seqs));
-  const int S = max((total + p.nwg - 1) / p.nwg, p.min_steps);
-  const int s0 = static_cast<int>(blockIdx.x) * S;
+  // ---- this workgroup's kv head and run of columns [s0, s1)
+  const int h = static_cast<int>(blockIdx.x) % p.Hkv;
+  const int run = static_cast<int>(blockIdx.x) / p.Hkv;
+  const int total = __builtin_amdgcn_readfirstlane(cols_before<STORE>(p, p.num_seqs));
+  const int S = max((total + p.nwg / p.Hkv - 1) / (p.nwg / p.Hkv), p.min_steps);
+  const int s0 = run * S;
   if (s0 >= total) return;
   const int s1 = min(s0 + S, total);
   int b, first;
-  locate(p, s0, b, first);
+  locate<STORE>(p, s0, b, first);
   b = __builtin_amdgcn_readfirstlane(b);
   first = __builtin_amdgcn_readfirstlane(first);
 
-  SeqInfo si = seq_info(p, b);
-  int n = steps_of(si.L);  // steps of every pair of sequence b
-  int h = (s0 - first) / n;
-  int j = s0 - first - h * n;
-  int j_first = j;  // step at which this workgroup entered the current pair
+  SeqInfo si = seq_info<STORE>(p, b);
+  int n = steps_of(si.L);  // columns of sequence b
+  int j = s0 - first;
+  int j_first = j;  // column at which this workgroup entered the current pair
 
   // ---- per-pair state: Q operand, causal limits, online-softmax state
   u32x4 qop[RT][4];
@@ -308,7 +333,7 @@ void paged_attn_main(AttnParams p) {
       const int qi = row / p.G, g = row - qi * p.G;
       const int64_t qt = si.q0 + qi;
       const bool valid = row < si.R && qt >= 0 && qt < p.total_q;
-      lim[rt] = valid ? si.L - si.nq + qi : -1;
+      lim[rt] = valid ? min(si.causal + qi, si.L - 1) : -1;
       const uint16_t* qp =
           p.q + (valid ? qt * p.q_stok + static_cast<int64_t>(h * p.G + g) * p.q_shead : 0) +
           lg * 8;
@@ -337,38 +362,6 @@ void paged_attn_main(AttnParams p) {
     const int32_t* btrow = p.bt + static_cast<int64_t>(lb) * p.bt_stride;
     const int64_t hoff = static_cast<int64_t>(lh) * p.c_shead;
     const bool used = real && lj * kTile + wave * kStep <= last;  // wave-uniform
-    // fused store: the sequence's last nq keys are this launch's new rows; a
-    // step that holds some reads them from knew / vnew (bits identical to what
-    // the store writes) and loads their slots beside them; compute_step swaps
-    // in the cache row for a new row whose slot is -1 (never written: the key
-    // stays the cache row, as without the store). Page lookups stay uniform;
-    // only the lanes of new rows swap their address.
-    int64_t q0 = 0;
-    int first_new = L;
-    bool fresh_step = false;
-    if constexpr (STORE) {
-      // only a step within max_qlen keys of the end can hold new rows
-      int slot_at = 0;
-      if (used && t0 + kStep > L - p.max_qlen) {
-        int nq;
-        seq_rows_uniform(p, lb, q0, nq);
-        first_new = L - nq;
-        if (nq > 0 && t0 + kStep > first_new) {
-          fresh_step = true;
-          slot_at = static_cast<int>(q0) + min(lane & 31, nq - 1);
-        }
-      }
-      // issued on every step (slot 0 when unused), like the K/V loads, so the
-      // count of loads in flight is the same on every path
-      R.slotv = p.slot[slot_at];
-    }
-    auto fresh_ptrs = [&](int tok, const void*& ks, const void*& vs) {
-      const int jn = tok - first_new;
-      if (jn >= 0) {
-        ks = p.knew + (q0 + jn) * p.kn_stok + lh * p.kn_shead + lr * 8;
-        vs = p.vnew + (q0 + jn) * p.vn_stok + lh * p.vn_shead + lr * 8;
-      }
-    };
     if constexpr (ONE_PAGE) {
       // scalar page base + 32-bit lane offsets (key rows of one page)
       const int64_t base = kv_row<true>(p, btrow, t0) + hoff;
@@ -379,27 +372,16 @@ void paged_attn_main(AttnParams p) {
         const int tok = min(t0 + r * 4 + lg, last);
         const uint32_t off =  // bytes
             used ? (static_cast<uint32_t>(tok - t0) * p.c_spos32 + lr * 8) * 2u : 0u;
-        if (STORE && fresh_step) {
-          const void* ks = kpg + off;
-          const void* vs = vpg + off;
-          fresh_ptrs(tok, ks, vs);
-          R.k[r] = sd::load16_stream(ks);
-          R.v[r] = sd::load16_stream(vs);
-        } else {
-          R.k[r] = sd::load16_stream(kpg + off);
-          R.v[r] = sd::load16_stream(vpg + off);
-        }
+        R.k[r] = sd::load16_stream(kpg + off);
+        R.v[r] = sd::load16_stream(vpg + off);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         const int tok = min(t0 + r * 4 + lg, last);
         const int64_t off = used ? kv_row(p, btrow, tok) + hoff + lr * 8 : 0;
-        const void* ks = p.kc + off;
-        const void* vs = p.vc + off;
-        if (STORE && fresh_step) fresh_ptrs(tok, ks, vs);
-        R.k[r] = sd::load16_stream(ks);
-        R.v[r] = sd::load16_stream(vs);
+        R.k[r] = sd::load16_stream(p.kc + off);
+        R.v[r] = sd::load16_stream(p.vc + off);
       }
     }
   };
@@ -410,29 +392,6 @@ void paged_attn_main(AttnParams p) {
   auto compute_step = [&](StepRegs& R, int cj) {
     const int tb = cj * kTile + wave * kStep;
     if (tb >= si.L) return;
-    if constexpr (STORE) {
-      // new rows of this step whose slot is not stored: their key is the cache
-      // row (rare: the engine gives -1 only to rows without keys)
-      const int first_new = si.L - si.nq;
-      if (si.nq > 0 && tb + kStep > first_new) {
-        const int sl = R.slotv;
-        const uint32_t want = si.nq >= 32 ? ~0u : (1u << si.nq) - 1u;
-        const uint32_t ok = static_cast<uint32_t>(__ballot(sl >= 0 && sl < p.num_slots)) & want;
-        if (ok != want) {
-          const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
-#pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            const int tok = min(tb + r * 4 + lg, si.L - 1);
-            const int jn = tok - first_new;
-            if (jn >= 0 && !((ok >> jn) & 1u)) {
-              const int64_t row = kv_row(p, btrow, tok) + static_cast<int64_t>(h) * p.c_shead + lr * 8;
-              R.k[r] = sd::load16(p.kc + row);
-              R.v[r] = sd::load16(p.vc + row);
-            }
-          }
-        }
-      }
-    }
     // ---- stage the 32 K and V rows of this step (row-major, padded pitch)
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -461,7 +420,7 @@ void paged_attn_main(AttnParams p) {
     //      and key 16 + 4 lg + (j - 4) (j >= 4), the order S^T already holds.
     u32x4 pop[RT], plo[RT];
     // every row sees every key of this slice: no causal / length mask needed
-    const bool full = tb + kStep - 1 <= si.L - si.nq;
+    const bool full = tb + kStep - 1 <= min(si.causal, si.L - 1);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       float mloc = -INFINITY;
@@ -553,7 +512,7 @@ void paged_attn_main(AttnParams p) {
     }
     __syncthreads();
     const int nrows = min(si.R, RT * 16);
-    const int64_t wslot = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(b) * p.Hkv + h;
+    const int64_t wslot = (static_cast<int64_t>(run) + b) * p.Hkv + h;
     for (int idx = tid; idx < nrows * 32; idx += kThreads) {
       const int row = idx >> 5, d4 = (idx & 31) * 4;
       const int qi = row / p.G, g = row - qi * p.G;
@@ -599,35 +558,28 @@ void paged_attn_main(AttnParams p) {
   int s = s0;
   auto advance = [&](StepRegs& cur, StepRegs& nxt) -> bool {
     // position of step s + 1
-    int nb = b, nh = h, nj = j + 1;
+    int nb = b, nj = j + 1;
     int nL = si.L;
     const bool more = s + 1 < s1;
-    if (more) {
-      if (nj == n) {
-        nj = 0;
-        if (++nh == p.Hkv) {
-          nh = 0;
-          do {
-            ++nb;
-            nL = seq_keys_uniform(p, nb);
-          } while (nL == 0);  // sequences without keys own no steps; s + 1 < total ends the scan
-        }
-      }
+    if (more && nj == n) {
+      nj = 0;
+      do {
+        ++nb;
+        nL = walk_keys_uniform<STORE>(p, nb);
+      } while (nL == 0);  // sequences without keys own no columns; s + 1 < total ends the scan
     }
     // the last step issues a dummy prefetch so that every iteration issues the
     // same loads
-    load_step(nxt, more ? nb : b, more ? nh : h, more ? nj : j, more ? nL : si.L, more);
+    load_step(nxt, more ? nb : b, h, more ? nj : j, more ? nL : si.L, more);
     compute_step(cur, j);
     const bool pair_end = j + 1 == n;
-    if (pair_end || !more) flush(pair_end && j_first == 0);
+    // STORE: partials only; the combine adds the new rows' keys
+    if (pair_end || !more) flush(!STORE && pair_end && j_first == 0);
     if (!more) return false;
-    if (nb != b || nh != h) {
-      if (nb != b) {
-        b = nb;
-        si = seq_info(p, b);
-        n = steps_of(si.L);
-      }
-      h = nh;
+    if (nb != b) {
+      b = nb;
+      si = seq_info<STORE>(p, b);
+      n = steps_of(si.L);
       j_first = 0;
       begin_pair();
     }
@@ -641,69 +593,118 @@ void paged_attn_main(AttnParams p) {
   }
 }
 
+// Four consecutive 16-bit elements as fp32.
+template <typename T>
+__device__ __forceinline__ f32x4 load4f(const uint16_t* src) {
+  const uint2 w = *reinterpret_cast<const uint2*>(src);
+  return f32x4{sd::from_bits<T>(static_cast<uint16_t>(w.x)), sd::from_bits<T>(static_cast<uint16_t>(w.x >> 16)),
+               sd::from_bits<T>(static_cast<uint16_t>(w.y)), sd::from_bits<T>(static_cast<uint16_t>(w.y >> 16))};
+}
+
 // Log-sum-exp merge of the partials of pair (b, h) = (blockIdx.z, blockIdx.y),
 // rows blockIdx.x * 8 .. +8 (one thread per row and 4 dims), zero rows for
-// sequences without keys. The pair spans global steps [f, f + n); the
-// workgroups that met it are f / S .. (f + n - 1) / S and workgroup w wrote
-// its partial to slot w + pair. A pair met by one workgroup is already final.
-template <typename T>
+// sequences without keys. Sequence b spans columns [f, f + n); the runs
+// that met it are f / S .. (f + n - 1) / S and run r's workgroup of head h
+// wrote its partial to slot (r + b) * Hkv + h. Without STORE a pair met by one
+// run is already final. STORE: every run wrote a partial of the cached keys,
+// and the sequence's n_b new keys (new row j at position L - n_b + j, seen by
+// query rows qi >= j) are merged here: s_j = q . k_j from the 16-bit inputs in
+// fp32, k_j / v_j from key / value — or from the cache row when the row's slot
+// is not stored (-1 or outside the pool), as an unfused store would leave it.
+template <typename T, bool STORE>
 __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   constexpr int kUnroll = 16;
   const int h = blockIdx.y, b = blockIdx.z;
-  const SeqInfo si = seq_info(p, b);
+  const SeqInfo si = seq_info<STORE>(p, b);
   const int row = blockIdx.x * (kThreads / 32) + (threadIdx.x >> 5);
   const int d4 = (threadIdx.x & 31) * 4;
-  const int total = steps_before(p, p.num_seqs);
-  const int first_b = steps_before(p, b);
+  const int total = cols_before<STORE>(p, p.num_seqs);
+  const int f = cols_before<STORE>(p, b);
   if (row >= si.R) return;
   const int qi = row / p.G, g = row - qi * p.G;
   const int64_t qt = si.q0 + qi;
   if (qt < 0 || qt >= p.total_q) return;
   uint16_t* op = p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + d4;
   const int n = steps_of(si.L);
-  if (n == 0) {
+  if (!STORE && n == 0) {
     *reinterpret_cast<uint2*>(op) = make_uint2(0u, 0u);
     return;
   }
-  const int S = max((total + p.nwg - 1) / p.nwg, p.min_steps);
-  const int f = first_b + h * n;
-  const int w0 = f / S, w1 = (f + n - 1) / S;
-  if (w0 == w1) return;
-  const float2* ml = reinterpret_cast<const float2*>(p.ws_ml);
-  const int64_t base =
-      (static_cast<int64_t>(w0) + static_cast<int64_t>(b) * p.Hkv + h) * p.rmax + row;
-  const int cnt = w1 - w0 + 1;
   float M = -INFINITY;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
   float l = 0.f;
-  for (int c0 = 0; c0 < cnt; c0 += kUnroll) {
-    float2 part[kUnroll];
-    f32x4 a[kUnroll];
+  if (n > 0) {
+    const int runs = p.nwg / p.Hkv;
+    const int S = max((total + runs - 1) / runs, p.min_steps);
+    const int w0 = f / S, w1 = (f + n - 1) / S;
+    if (!STORE && w0 == w1) return;
+    const float2* ml = reinterpret_cast<const float2*>(p.ws_ml);
+    const int64_t base = ((static_cast<int64_t>(w0) + b) * p.Hkv + h) * p.rmax + row;
+    const int64_t run_stride = static_cast<int64_t>(p.Hkv) * p.rmax;  // rows between runs
+    const int cnt = w1 - w0 + 1;
+    for (int c0 = 0; c0 < cnt; c0 += kUnroll) {
+      float2 part[kUnroll];
+      f32x4 a[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t e = base + static_cast<int64_t>(c0 + u) * p.rmax;
-      if (c0 + u < cnt) {
-        part[u] = ml[e];
-        a[u] = __builtin_bit_cast(f32x4, sd::load16(p.ws_acc + e * kD + d4));
-      } else {
-        part[u] = make_float2(-INFINITY, 0.f);
-        a[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t e = base + static_cast<int64_t>(c0 + u) * run_stride;
+        if (c0 + u < cnt) {
+          part[u] = ml[e];
+          a[u] = __builtin_bit_cast(f32x4, sd::load16(p.ws_acc + e * kD + d4));
+        } else {
+          part[u] = make_float2(-INFINITY, 0.f);
+          a[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
-    }
-    float mc = M;
+      float mc = M;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) mc = fmaxf(mc, part[u].x);
-    if (mc == -INFINITY) continue;
-    const float r = exp2f(M - mc);  // rescale what earlier batches summed
-    l *= r;
-    o *= r;
+      for (int u = 0; u < kUnroll; ++u) mc = fmaxf(mc, part[u].x);
+      if (mc == -INFINITY) continue;
+      const float r = exp2f(M - mc);  // rescale what earlier batches summed
+      l *= r;
+      o *= r;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const float w = exp2f(part[u].x - mc);
-      l += w * part[u].y;
-      o += w * a[u];
+      for (int u = 0; u < kUnroll; ++u) {
+        const float w = exp2f(part[u].x - mc);
+        l += w * part[u].y;
+        o += w * a[u];
+      }
+      M = mc;
     }
-    M = mc;
+  }
+  if constexpr (STORE) {
+    // the 32 lanes of this row hold 4 dims each; the dot products reduce over them
+    const int L = seq_keys(p, b);
+    const f32x4 qv =
+        load4f<T>(p.q + qt * p.q_stok + static_cast<int64_t>(h * p.G + g) * p.q_shead + d4);
+    const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
+    for (int j = 0; j < si.nq; ++j) {  // uniform over the row's lanes
+      const int pos = L - si.nq + j;
+      if (pos < 0 || j > qi) continue;
+      const int64_t tr = si.q0 + j;
+      const int64_t slot = p.slot[tr];
+      const uint16_t* kr;
+      const uint16_t* vr;
+      if (slot >= 0 && slot < p.num_slots) {
+        kr = p.knew + tr * p.kn_stok + static_cast<int64_t>(h) * p.kn_shead;
+        vr = p.vnew + tr * p.vn_stok + static_cast<int64_t>(h) * p.vn_shead;
+      } else {
+        const int64_t crow = kv_row(p, btrow, pos) + static_cast<int64_t>(h) * p.c_shead;
+        kr = p.kc + crow;
+        vr = p.vc + crow;
+      }
+      const f32x4 kv = load4f<T>(kr + d4);
+      const f32x4 vv = load4f<T>(vr + d4);
+      float dot = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) dot += __shfl_xor(dot, off);
+      const float sj = dot * p.scale_log2;
+      const float mn = fmaxf(M, sj);
+      const float r = exp2f(M - mn), w = exp2f(sj - mn);
+      l = l * r + w;
+      o = o * r + w * vv;
+      M = mn;
+    }
   }
   store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);
 }
@@ -712,7 +713,7 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
 template <typename T, bool STORE>
 __global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
   if constexpr (!STORE) {
-    combine_rows<T>(p);
+    combine_rows<T, false>(p);
   } else {
     const uint32_t items = 2u * static_cast<uint32_t>(p.total_q) * p.Hkv * (kD * 2 / 16);
     const uint32_t nthreads = gridDim.x * gridDim.y * gridDim.z * kThreads;
@@ -723,7 +724,7 @@ __global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
       piece_of(p, it0, sp);
       load_piece(p, sp);
     }
-    combine_rows<T>(p);
+    combine_rows<T, true>(p);
     if (it0 < items) write_piece(p, sp);
     for (uint32_t it = it0 + nthreads; it < items; it += nthreads) {
       piece_of(p, it, sp);
@@ -736,10 +737,10 @@ __global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
 // ------------------------------------------------------------------ host
 struct Plan {
   int RT;         // 16-row tiles of query rows
-  int nwg;        // workgroups of the main grid
-  int min_steps;  // lower bound of steps per workgroup
+  int nwg;        // workgroups of the main grid: runs * Hkv
+  int min_steps;  // lower bound of columns per run
   int rmax;       // rows per (sequence, kv head) in the workspace
-  int64_t slots;  // partial slots: nwg + num_seqs * Hkv
+  int64_t slots;  // partial slots: (runs + num_seqs) * Hkv
 };
 
 // Compute units of the current device (cached per device id).
@@ -765,15 +766,18 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   const int G = Hq / Hkv;
   pl.rmax = G * max_qlen;
   pl.RT = pl.rmax <= 16 ? 1 : 2;
+  int64_t runs;
   if (num_splits > 0) {
-    const int64_t w = static_cast<int64_t>(num_splits) * num_seqs * Hkv;
-    pl.nwg = static_cast<int>(w < (1 << 20) ? w : (1 << 20));
+    runs = static_cast<int64_t>(num_splits) * num_seqs;
     pl.min_steps = 1;
   } else {
-    pl.nwg = device_cus() * (pl.RT == 1 ? main_occupancy<1>() : main_occupancy<2>());
+    runs = device_cus() * (pl.RT == 1 ? main_occupancy<1>() : main_occupancy<2>()) / Hkv;
     pl.min_steps = pl.RT == 1 ? 1 : 2;
   }
-  pl.slots = static_cast<int64_t>(pl.nwg) + static_cast<int64_t>(num_seqs) * Hkv;
+  const int64_t cap = (1 << 20) / Hkv > 1 ? (1 << 20) / Hkv : 1;  // grid of at most ~2^20
+  runs = runs < 1 ? 1 : (runs > cap ? cap : runs);
+  pl.nwg = static_cast<int>(runs * Hkv);
+  pl.slots = (runs + num_seqs) * Hkv;
   return pl;
 }
 

@@ -100,9 +100,11 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
 
     ``key``/``value`` (total_q, num_kv_heads, head_dim) with ``slot_mapping``
     (total_q,): store_kvcache of these rows fused into the same launch — the
-    ``Attention.forward`` sequence (nanovllm/layers/attention.py:59-82). Same
-    cache and output as ``store_kvcache`` then attention, for the engine's slot
-    layout: sequence b's rows are its last n_b keys (slot -1: not written).
+    ``Attention.forward`` sequence (nanovllm/layers/attention.py:59-82). The
+    same cache as ``store_kvcache`` and the output of attention afterwards up to
+    rounding (the new keys are scored in fp32 in the merge launch), for the
+    engine's slot layout: sequence b's rows are its last n_b keys (slot -1: not
+    written).
     """
     if q.dim() != 3:
         raise ValueError(f"q must be (tokens, heads, head_dim), got {tuple(q.shape)}")
