@@ -50,6 +50,7 @@ struct W8Params {
   int32_t M, N, K;
   int32_t nks;     // K / 64
   int32_t groups;  // row groups of 16 NT rows
+  int32_t xpitch;  // bytes per activation row in LDS (staged activations only)
 };
 
 __device__ __forceinline__ float load_scale(const void* s, int dtype, int64_t i) {
@@ -108,8 +109,15 @@ template <> __device__ __forceinline__ u32x4 dequant8<__bf16>(uint32_t w0, uint3
 // (SWZ = min(4 U, 16) - 1), from which each lane reads its MFMA A operand
 // (16 int8 of row l % 16 at k = 64 step + 16 (l / 16)) with ds_read_b128; with
 // 16 positions per row the 16 lanes of a read hit distinct banks.
+//
+// XL: the workgroup's activation rows (whole K) are staged in LDS once, at
+// the start, and each step's B operand is read from there. The only vector
+// loads left in the loop are the weight stream's: for M = 1 the activation
+// loads were as many instructions per chunk as the weight loads (4 of 64
+// lanes active), and every vector load instruction costs the compute unit's
+// address path the same time whatever its lane count.
 template <typename T, int MT, int NT, int KW, int U, bool PER_GROUP, bool CONTIG = false,
-          int D = 2>
+          int D = 2, bool XL = false>
 __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
   static_assert(U == 2 || U == 4 || U == 8, "a chunk row segment is 64 U bytes");
   constexpr int LPR = 4 * U;         // lanes per row segment (16-byte units per row)
@@ -120,6 +128,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
   constexpr int TILE = 16 * NT * LPR * 16;  // bytes of one wave's LDS tile
   __shared__ __attribute__((aligned(16))) char wtile[kWaves][TILE];
   __shared__ __attribute__((aligned(16))) float red[KW > 1 ? KW - 1 : 1][NT * MT * 4][64];
+  extern __shared__ __attribute__((aligned(16))) char xsm[];  // XL: activation rows
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -150,7 +159,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
     ngroups = g0 < p.groups ? (p.groups - g0 + gstride - 1) / gstride : 0;
   }
   const int nit = ngroups * nchunks;
-  if (nit == 0) return;  // uniform over the workgroup when KW > 1 (NSUB == 1)
+  if (!XL && nit == 0) return;  // uniform over the workgroup when KW > 1 (NSUB == 1)
 
   // Activation rows past M are never loaded: those lanes keep zeros (only the
   // lanes of real rows touch memory, e.g. 4 of 64 at M = 1).
@@ -175,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 
   struct Regs {
     u32x4 w[NLD];
-    u32x4 x[U][MT][2];  // activation B operands of the chunk's steps
+    u32x4 x[XL ? 1 : U][MT][2];  // activation B operands of the chunk's steps (not XL)
   };
   // Every call issues the same loads: steps past this wave's K range are
   // clamped into the matrix (loaded, never used), rows past N / M read a valid
@@ -195,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
       R.w[i] = sd::load16_stream(real ? p.w + static_cast<int64_t>(n) * p.ws + kw_off : p.w);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < (XL ? 0 : U); ++u) {
       const int64_t k0 = static_cast<int64_t>(min(s0 + u, p.nks - 1)) * 64;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -225,7 +234,23 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
       const int step = s0 + u;
       if (step >= ke) break;  // wave-uniform
       const int64_t k0 = static_cast<int64_t>(step) * 64;
-      const u32x4(&xv)[MT][2] = R.x[u];
+      u32x4 xv[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (XL) {
+          if (xok[mt]) {
+            const char* xr = xsm + (mt * 16 + lr) * p.xpitch + step * 128 + lg * 32;
+            xv[mt][0] = sd::load16(xr);
+            xv[mt][1] = sd::load16(xr + 16);
+          } else {
+            xv[mt][0] = u32x4{0u, 0u, 0u, 0u};
+            xv[mt][1] = u32x4{0u, 0u, 0u, 0u};
+          }
+        } else {
+          xv[mt][0] = R.x[u][mt][0];
+          xv[mt][1] = R.x[u][mt][1];
+        }
+      }
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int r = nt * 16 + lr;
@@ -325,8 +350,22 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
   auto group_of = [&](int i) { return g0 + (i / nchunks) * gstride; };
 #pragma unroll
   for (int d = 0; d < D - 1; ++d) {
+    if (XL && nit == 0) break;
     const int i = min(d, nit - 1);
     load(ring[d], group_of(i), i % nchunks, d < nit);
+  }
+  if constexpr (XL) {
+    // stage rows m0 .. m0 + rows of x (16-byte units) behind the first weight
+    // prefetch, so their latencies overlap; every wave of the workgroup takes part
+    const int rows = min(MT * 16, p.M - m0);
+    const int upr = p.K / 8;  // 16-byte units per row
+    for (int idx = tid; idx < rows * upr; idx += kThreads) {
+      const int r = idx / upr, c = idx - r * upr;
+      sd::store16(xsm + r * p.xpitch + c * 16,
+                  sd::load16(p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8));
+    }
+    __syncthreads();
+    if (nit == 0) return;
   }
   for (int it = 0; it < nit; it += D) {
 #pragma unroll
@@ -377,7 +416,9 @@ W8Plan make_plan(int64_t M, int64_t N, int64_t K) {
   // rows: the measured best for the narrow layers at every M).
   if (nr * pl.mblocks >= 8ll * cus || nks < 4) {
     pl.KW = 1;
-    pl.NT = nr < 2 ? 1 : 2;
+    // 16-row groups balance better over the waves (lm_head M = 1: 29.0 vs
+    // 30.0 us); from M = 8 up, 32-row groups reuse each activation read twice
+    pl.NT = nr < 2 || M <= 4 ? 1 : 2;
   } else {
     pl.KW = 4;
     pl.NT = 1;
@@ -405,9 +446,43 @@ int resident_wgs(Kern kern) {
   return n;
 }
 
+// Activation rows staged in LDS (XL, 16-row blocks only: 32 staged rows cost
+// more in occupancy than they save): bytes per row pad and the most a
+// workgroup stages (16 rows of K <= 1024).
+constexpr int kXPad = 16;
+constexpr int kXlMaxBytes = 16 * (1024 * 2 + kXPad);
+
+// Resident workgroups per CU of an XL kernel with `smem` bytes of dynamic LDS
+// (cached per device and activation row count).
+template <typename Kern>
+int resident_wgs_xl(Kern kern, int rows, size_t smem) {
+  static int cache[64][33] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const bool ok = dev >= 0 && dev < 64 && rows >= 1 && rows <= 32;
+  if (ok && cache[dev][rows] > 0) return cache[dev][rows];
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, smem) != hipSuccess || n <= 0)
+    n = 1;
+  if (ok) cache[dev][rows] = n;
+  return n;
+}
+
 template <typename T, int MT, int NT, int KW, bool PG>
 void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
   constexpr int U = NT >= 2 ? 2 : 4;  // 64-k steps per chunk
+  if constexpr (KW == 1) {
+    const int rows = static_cast<int>(p.M < MT * 16 ? p.M : MT * 16);
+    const size_t smem = static_cast<size_t>(rows) * p.xpitch;
+    if (MT == 1 && p.xpitch > 0 && smem <= static_cast<size_t>(kXlMaxBytes)) {
+      auto kern = w8a16_kernel<T, MT, NT, KW, U, PG, false, 2, true>;
+      unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs_xl(kern, rows, smem)) / grid.y;
+      cap = cap >= 8 ? cap / 8 * 8 : 1;
+      if (grid.x > cap) grid.x = cap;
+      hipLaunchKernelGGL(kern, grid, dim3(kThreads), smem, st, p);
+      return;
+    }
+  }
   auto kern = w8a16_kernel<T, MT, NT, KW, U, PG>;
   // exactly one resident set of workgroups over all activation blocks (a
   // partial second round would leave most of the GPU idle at the end), grid.x
@@ -515,6 +590,9 @@ extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* 
   p.K = static_cast<int32_t>(K);
   p.nks = static_cast<int32_t>(K / 64);
   p.groups = pl.groups;
+  // staged activation rows (wide path): K * 2 bytes + a 16-byte pad per row, so
+  // that the 16 rows of a B-operand read start 4 banks apart
+  p.xpitch = K * 2 + kXPad <= 1024 * 2 + kXPad ? static_cast<int32_t>(K * 2 + kXPad) : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == SD_BF16) return launch_all<__bf16>(p, pl, st);
   return launch_all<_Float16>(p, pl, st);
