@@ -51,6 +51,8 @@ struct W8Params {
   int32_t nks;     // K / 64
   int32_t groups;  // row groups of 16 NT rows
   int32_t xpitch;  // bytes per activation row in LDS (staged activations only)
+  int32_t xbytes;  // XL: bytes of staged activation rows; the scale table follows
+  int32_t ngmax;   // XL: most row groups one wave owns
 };
 
 __device__ __forceinline__ float load_scale(const void* s, int dtype, int64_t i) {
@@ -161,6 +163,16 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
   const int nit = ngroups * nchunks;
   if (!XL && nit == 0) return;  // uniform over the workgroup when KW > 1 (NSUB == 1)
 
+  // XL: fp32 scale table (and bias) of every row this workgroup's waves own, in
+  // LDS after the activation rows: [sub][group of the wave][row][scale column]
+  constexpr int RG = NT * 16;  // rows per group
+  const int spr = PER_GROUP ? p.K / p.group : 1;
+  float* scl = reinterpret_cast<float*>(xsm + p.xbytes);
+  float* bis = scl + NSUB * p.ngmax * RG * spr;
+  auto srow = [&](int g, int r) {  // scale-table row of row r of group g (this wave's)
+    return (sub * p.ngmax + (g - g0) / gstride) * RG + r;
+  };
+
   // Activation rows past M are never loaded: those lanes keep zeros (only the
   // lanes of real rows touch memory, e.g. 4 of 64 at M = 1).
   const uint16_t* xp[MT];
@@ -269,8 +281,12 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
           float sc[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int n = min(n0 + nt * 16 + lg * 4 + i, p.N - 1);
-            sc[i] = load_scale(p.scale, p.scale_dtype, static_cast<int64_t>(n) * ng + grp);
+            if constexpr (XL) {
+              sc[i] = scl[srow(g, nt * 16 + lg * 4 + i) * spr + grp];
+            } else {
+              const int n = min(n0 + nt * 16 + lg * 4 + i, p.N - 1);
+              sc[i] = load_scale(p.scale, p.scale_dtype, static_cast<int64_t>(n) * ng + grp);
+            }
           }
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
@@ -323,8 +339,16 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int n = min(nb + i, p.N - 1);
-            const float sc = PER_GROUP ? 1.f : load_scale(p.scale, p.scale_dtype, n);
-            v[i] = acc[nt][mt][i] * sc + (p.bias ? sd::from_bits<T>(p.bias[n]) : 0.f);
+            float sc, bi;
+            if constexpr (XL) {
+              const int sr = srow(g, nt * 16 + lg * 4 + i);
+              sc = PER_GROUP ? 1.f : scl[sr];
+              bi = p.bias ? bis[sr] : 0.f;
+            } else {
+              sc = PER_GROUP ? 1.f : load_scale(p.scale, p.scale_dtype, n);
+              bi = p.bias ? sd::from_bits<T>(p.bias[n]) : 0.f;
+            }
+            v[i] = acc[nt][mt][i] * sc + bi;
           }
           uint16_t* dst = p.y + static_cast<int64_t>(m) * p.ys + nb;
           if (nb + 3 < p.N && (reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
@@ -363,6 +387,23 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
       const int r = idx / upr, c = idx - r * upr;
       sd::store16(xsm + r * p.xpitch + c * 16,
                   sd::load16(p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8));
+    }
+    // scales (and bias) of the rows every wave of this workgroup owns
+    const int per_sub = p.ngmax * RG;
+    for (int idx = tid; idx < NSUB * per_sub * spr; idx += kThreads) {
+      const int j = idx % spr, t = idx / spr;
+      const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
+      const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
+      const int n = min(g * RG + r, p.N - 1);
+      scl[idx] = load_scale(p.scale, p.scale_dtype,
+                            PER_GROUP ? static_cast<int64_t>(n) * spr + j : n);
+    }
+    if (p.bias) {
+      for (int t = tid; t < NSUB * per_sub; t += kThreads) {
+        const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
+        const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
+        bis[t] = sd::from_bits<T>(p.bias[min(g * RG + r, p.N - 1)]);
+      }
     }
     __syncthreads();
     if (nit == 0) return;
@@ -451,6 +492,8 @@ int resident_wgs(Kern kern) {
 // workgroup stages (16 rows of K <= 1024).
 constexpr int kXPad = 16;
 constexpr int kXlMaxBytes = 16 * (1024 * 2 + kXPad);
+// The most LDS the scale table may take (per group and bias included).
+constexpr int kXlScaleBytes = 32 * 1024;
 
 // Resident workgroups per CU of an XL kernel with `smem` bytes of dynamic LDS
 // (cached per device and activation row count).
@@ -473,14 +516,24 @@ void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
   constexpr int U = NT >= 2 ? 2 : 4;  // 64-k steps per chunk
   if constexpr (KW == 1) {
     const int rows = static_cast<int>(p.M < MT * 16 ? p.M : MT * 16);
-    const size_t smem = static_cast<size_t>(rows) * p.xpitch;
-    if (MT == 1 && p.xpitch > 0 && smem <= static_cast<size_t>(kXlMaxBytes)) {
+    const size_t xbytes = static_cast<size_t>(rows) * p.xpitch;
+    if (MT == 1 && p.xpitch > 0 && xbytes <= static_cast<size_t>(kXlMaxBytes)) {
       auto kern = w8a16_kernel<T, MT, NT, KW, U, PG, false, 2, true>;
-      unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs_xl(kern, rows, smem)) / grid.y;
+      // occupancy from the activation rows; the scale table adds a few KB (per
+      // channel: 16 B per row of the workgroup)
+      unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs_xl(kern, rows, xbytes)) /
+                     grid.y;
       cap = cap >= 8 ? cap / 8 * 8 : 1;
       if (grid.x > cap) grid.x = cap;
-      hipLaunchKernelGGL(kern, grid, dim3(kThreads), smem, st, p);
-      return;
+      W8Params q = p;
+      q.xbytes = static_cast<int32_t>((xbytes + 15) / 16 * 16);
+      q.ngmax = (p.groups + static_cast<int>(grid.x) * kWaves - 1) / (static_cast<int>(grid.x) * kWaves);
+      const size_t spr = PG ? static_cast<size_t>(p.K / p.group) : 1;
+      const size_t tbl = static_cast<size_t>(kWaves) * q.ngmax * NT * 16 * (spr + (p.bias ? 1 : 0)) * 4;
+      if (tbl <= static_cast<size_t>(kXlScaleBytes)) {
+        hipLaunchKernelGGL(kern, grid, dim3(kThreads), q.xbytes + tbl, st, q);
+        return;
+      }
     }
   }
   auto kern = w8a16_kernel<T, MT, NT, KW, U, PG>;
@@ -593,6 +646,8 @@ extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* 
   // staged activation rows (wide path): K * 2 bytes + a 16-byte pad per row, so
   // that the 16 rows of a B-operand read start 4 banks apart
   p.xpitch = K * 2 + kXPad <= 1024 * 2 + kXPad ? static_cast<int32_t>(K * 2 + kXPad) : 0;
+  p.xbytes = 0;
+  p.ngmax = 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == SD_BF16) return launch_all<__bf16>(p, pl, st);
   return launch_all<_Float16>(p, pl, st);

@@ -75,6 +75,22 @@ def test_ragged_shapes_and_bias(M, N, K):
     check(y, c["x"], c["w"], c["s"], bias, what=f"{M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M", [1, 3, 12])
+@pytest.mark.parametrize("gs", [0, 64, 128])
+def test_wide_path_scales_and_bias(M, gs):
+    # N = 33000 rows of K = 1024: the wide path (whole rows per wave, activation rows and
+    # the row groups' scales and bias staged in LDS), ragged last row group, fp32 scales
+    N, K = 33000, 1024
+    c = workloads.w8a16_case(M, N, K, seed=M + gs)
+    g = workloads.device_generator(DEV, 11)
+    shape = (N,) if gs == 0 else (N, K // gs)
+    s = (torch.rand(shape, generator=g, device=DEV) * 3e-3 + 1e-3).to(torch.float32)
+    bias = torch.randn((N,), generator=g, device=DEV).to(torch.float16)
+    y = ops.w8a16_linear(c["x"], c["w"], s, bias, group_size=gs)
+    check(y, c["x"], c["w"], s, bias, gran="per_group" if gs else "per_channel", gs=gs or 128,
+          what=f"wide M={M} group={gs}")
+
+
 def test_full_int8_range_including_minus_128():
     M, N, K = 4, 256, 512
     w = torch.arange(N * K, device=DEV).remainder(256).sub(128).to(torch.int8).view(N, K)
