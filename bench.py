@@ -318,11 +318,37 @@ def profile_pass(ops, workloads, torch):
     c = workloads.w8a16_case(1, 151936, 1024, seed=1)
     for _ in range(3):
         ops.w8a16_linear(c["x"], c["w"], c["s"])
+    del src, dst
+    # the kernels where MFMA does the contraction (for the MFMA-utilization pass):
+    # C3 verify (fused store), lm_head at M = 56, prefill; in this order, 3 each
+    v = workloads.verify_case(seed=0)
+    vt, vcu_k, vcu_q, vsl = v["table"].cuda(), v["cu_k"].cuda(), v["cu_q"].cuda(), v["slots"].cuda()
+    vo = torch.empty_like(v["q"])
+    for _ in range(3):
+        ops.paged_attention(v["q"], v["k_cache"], v["v_cache"], vt, v["scale"],
+                            cu_seqlens_k=vcu_k, cu_seqlens_q=vcu_q, max_seqlen_q=v["k"] + 1,
+                            out=vo, key=v["k_new"], value=v["v_new"], slot_mapping=vsl)
+    c56 = workloads.w8a16_case(56, 151936, 1024, seed=2)
+    for _ in range(3):
+        ops.w8a16_linear(c56["x"], c56["w"], c56["s"])
+    B, L, hq, hkv = 4, 2048, 32, 8
+    g = torch.Generator(device="cuda").manual_seed(5)
+    pq = torch.randn((B * L, hq, 128), generator=g, device="cuda").to(torch.bfloat16)
+    pk = torch.randn((B * L, hkv, 128), generator=g, device="cuda").to(torch.bfloat16)
+    pv = torch.randn((B * L, hkv, 128), generator=g, device="cuda").to(torch.bfloat16)
+    cu = torch.arange(0, (B + 1) * L, L, dtype=torch.int32, device="cuda")
+    po = torch.empty_like(pq)
+    for _ in range(3):
+        ops.prefill_attention(pq, pk, pv, cu, cu, L, 128 ** -0.5, out=po)
     torch.cuda.synchronize()
     print(json.dumps({"profile_pass": True, "attn_bytes": attn_bytes(case["lens"].tolist(),
                                                                      32, 8, 128, 2),
-                      "copy_bytes": 2 * src.numel(),
-                      "lm_head_bytes": 151936 * 1024 + 2 * 151936 + 2048 + 2 * 151936}))
+                      "copy_bytes": 2 * 512 * 2 ** 20,
+                      "lm_head_bytes": 151936 * 1024 + 2 * 151936 + 2048 + 2 * 151936,
+                      "verify_flops": 4 * 128 * hq * sum(
+                          sum(int(K) - v["k"] + i for i in range(v["k"] + 1)) for K in v["keys"]),
+                      "lm_head_m56_flops": 2 * 56 * 151936 * 1024,
+                      "prefill_flops": 4 * 128 * hq * B * L * (L + 1) // 2}))
 
 
 # ------------------------------------------------------------------------------- main
