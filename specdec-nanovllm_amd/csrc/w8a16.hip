@@ -487,11 +487,10 @@ int resident_wgs(Kern kern) {
   return n;
 }
 
-// Activation rows staged in LDS (XL, 16-row blocks only: 32 staged rows cost
-// more in occupancy than they save): bytes per row pad and the most a
-// workgroup stages (16 rows of K <= 1024).
+// Activation rows staged in LDS (XL): bytes per row pad and the most a
+// workgroup stages (32 rows of K <= 1024).
 constexpr int kXPad = 16;
-constexpr int kXlMaxBytes = 16 * (1024 * 2 + kXPad);
+constexpr int kXlMaxBytes = 32 * (1024 * 2 + kXPad);
 // The most LDS the scale table may take (per group and bias included).
 constexpr int kXlScaleBytes = 32 * 1024;
 
@@ -517,8 +516,11 @@ void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
   if constexpr (KW == 1) {
     const int rows = static_cast<int>(p.M < MT * 16 ? p.M : MT * 16);
     const size_t xbytes = static_cast<size_t>(rows) * p.xpitch;
-    if (MT == 1 && p.xpitch > 0 && xbytes <= static_cast<size_t>(kXlMaxBytes)) {
-      auto kern = w8a16_kernel<T, MT, NT, KW, U, PG, false, 2, true>;
+    if (p.xpitch > 0 && xbytes <= static_cast<size_t>(kXlMaxBytes)) {
+      // 32 staged rows leave LDS for one workgroup per CU: 8-step chunks (16 KB
+      // per wave at NT = 2) keep enough of the weight stream in flight
+      constexpr int UX = MT == 2 ? 8 : U;
+      auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true>;
       // occupancy from the activation rows; the scale table adds a few KB (per
       // channel: 16 B per row of the workgroup)
       unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs_xl(kern, rows, xbytes)) /
