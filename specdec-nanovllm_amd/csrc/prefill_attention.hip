@@ -108,7 +108,12 @@ void prefill_kernel(PrefillParams p) {
   const int t0 = (SPLIT ? static_cast<int>(blockIdx.x)
                         : static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * tpw;
   if (t0 >= nq) return;
-  if (SPLIT != (nk - nq + t0 + 1 < kSplitKeys)) return;  // the other instance's tile
+  // the split instance covers the first split_tiles tiles; a tile there whose
+  // first token sees fewer than kSplitKeys keys is its, every other tile is
+  // the single-P instance's (also when nk < nq leaves later tiles short of keys)
+  const int split_tiles = (kSplitKeys + tpw - 1) / tpw;
+  const bool want_split = t0 < split_tiles * tpw && nk - nq + t0 + 1 < kSplitKeys;
+  if (SPLIT != want_split) return;  // the other instance's tile
   const int tl = min(t0 + tpw, nq) - 1;  // last token of the tile
   const int32_t* btrow = p.bt ? p.bt + static_cast<int64_t>(b) * p.bt_stride : nullptr;
   const int64_t hoff = static_cast<int64_t>(h) * p.s_head;

@@ -76,6 +76,22 @@ def test_more_keys_than_queries_and_empty_sequences():
     assert_close_attn(to_np(o.float()), ref_varlen(q, k, v, cu_q, cu_k, 0.1), what="nk > nq")
 
 
+def test_fewer_keys_than_queries():
+    # nk < nq: under the bottom-right rule the first nq - nk rows see no key (zeros) and
+    # the rest see a growing prefix; tiles past the few-key tiles still run
+    lq, lk = [600, 40], [500, 1]
+    q, k, v, cu_q, cu_k = make(lq, lk, 32, 8, seed=13)
+    o = to_np(ops.prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu_q.to(DEV),
+                                    cu_k.to(DEV), max(lq), 0.1).float())
+    ref = ref_varlen(q, k, v, cu_q, cu_k, 0.1)
+    seen = np.zeros(sum(lq), dtype=bool)  # rows that see at least one key
+    for b in range(len(lq)):
+        t = np.arange(lq[b])
+        seen[int(cu_q[b]) + t] = lk[b] - lq[b] + t >= 0
+    assert np.all(o[~seen] == 0)
+    assert_close_attn(o[seen], ref[seen], what="nk < nq")
+
+
 def _paged(k, v, cu_k, bs, seed):
     """Scatter contiguous k/v rows into a shuffled page pool; returns caches + table."""
     lens = (cu_k[1:] - cu_k[:-1]).tolist()
