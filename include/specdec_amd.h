@@ -270,8 +270,9 @@ int sd_silu_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride, 
  *   index among equal maxima, as torch.argmax).
  *   otherwise: argmax(softmax(l / T) / E), E ~ Exp(1), computed as
  *   argmax(l / T - log E) with E = max(-log U, 1e-10), U in (0, 1] from
- *   Philox4x32-10 keyed by rng_state[0] (seed) with counter (column,
- *   row ^ high word of rng_state[1], low word of rng_state[1], 0).
+ *   word (column % 4) of the Philox4x32-10 block keyed by rng_state[0] (seed)
+ *   with counter (column / 4, row ^ high word of rng_state[1], low word of
+ *   rng_state[1], 0).
  *   rng_state: (2,) int64 on the device, read only; the caller advances the
  *   offset between calls (on the stream, so graph replays advance it too).
  */
@@ -293,7 +294,7 @@ int sd_sample(const void* logits, int64_t logits_stride, int32_t dtype, int64_t 
  *         num_kv_heads, 128) by kv_stride_block / kv_stride_tok /
  *         kv_stride_head (the prefix-cache case)
  *   out : (total_q, num_q_heads, 128)
- * head_dim 128, num_q_heads / num_kv_heads dividing 64, bf16/f16; 16-byte
+ * head_dim 128, num_q_heads / num_kv_heads dividing 128, bf16/f16; 16-byte
  * aligned rows. One launch, no workspace.
  */
 int sd_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -329,7 +330,8 @@ size_t sd_verify_batch_workspace_size(int64_t batch, int32_t k, int32_t vocab);
  * normalize(max(0, p_a - q_a)) at a = accepted with q_k = 0 (p_a when the
  * residual is all zero); accept_mask (batch, k) uint8 per-candidate tests.
  * u_j and the bonus race noise come from Philox4x32-10 (streams 1 and 2 of
- * the counter's last word), so a call is a pure function of its inputs.
+ * the counter's last word; the bonus noise of column i is word i % 4 of the
+ * block with counter (i / 4, ...)), so a call is a pure function of its inputs.
  * Three launches (row statistics, acceptance + residual race, merge); k <= 32.
  */
 int sd_verify_batch(const void* draft, int64_t draft_stride_b, int64_t draft_stride_k,

@@ -114,9 +114,18 @@ def philox4x32_10(c0, c1, c2, c3, k0, k1):
     return c
 
 
+def element_words(idx, c1, c2, c3, seed):
+    """The 32-bit noise word of element idx: word idx % 4 of the Philox block
+    with counter (idx // 4, c1, c2, c3) (four elements per Philox call)."""
+    idx = np.asarray(idx, dtype=np.uint32)
+    r = philox4x32_10(idx >> np.uint32(2), c1, c2, c3, np.uint32(seed & 0xFFFFFFFF),
+                      np.uint32((seed >> 32) & 0xFFFFFFFF))
+    return np.choose((idx & np.uint32(3)).astype(np.int64), r)
+
+
 def sample_keys(logits, temperatures, seed, offset):
     """The per-element race keys: l / T - log(max(-log U, 1e-10)), U in (0, 1]
-    from Philox keyed by the seed with counter (column, row ^ offset_hi,
+    from element_words of column i with counter (i // 4, row ^ offset_hi,
     offset_lo, 0). argmax of these is the draw of sampler.py:6-12
     (argmax(softmax(l / T) / E), E = -log U ~ Exp(1))."""
     logits = np.asarray(logits, dtype=np.float32)
@@ -124,10 +133,9 @@ def sample_keys(logits, temperatures, seed, offset):
     col = np.broadcast_to(np.arange(V, dtype=np.uint32)[None, :], (rows, V))
     row = np.broadcast_to(np.arange(rows, dtype=np.uint32)[:, None], (rows, V))
     off_lo, off_hi = np.uint32(offset & 0xFFFFFFFF), np.uint32((offset >> 32) & 0xFFFFFFFF)
-    r = philox4x32_10(col, row ^ off_hi, np.full((rows, V), off_lo, np.uint32),
-                      np.zeros((rows, V), np.uint32), np.uint32(seed & 0xFFFFFFFF),
-                      np.uint32((seed >> 32) & 0xFFFFFFFF))
-    u = ((r[0] >> np.uint32(8)).astype(np.float32) + np.float32(1)) * np.float32(1.0 / 16777216.0)
+    w = element_words(col, row ^ off_hi, np.full((rows, V), off_lo, np.uint32),
+                      np.zeros((rows, V), np.uint32), seed)
+    u = ((w >> np.uint32(8)).astype(np.float32) + np.float32(1)) * np.float32(1.0 / 16777216.0)
     e = np.maximum(-np.log(u), np.float32(1e-10)).astype(np.float32)
     t = np.asarray(temperatures, dtype=np.float32)[:, None]
     return (logits * (np.float32(1) / t) - np.log(e)).astype(np.float32)
@@ -162,7 +170,8 @@ def verify_batch(draft, target, tokens, temperatures=None, point_mass=False, see
     when q_j[x_j] == 0), u_j = (Philox(j, b ^ off_hi, off_lo, 1).c0 >> 8) 2^-24;
     accepted = first failure (k if none); bonus = argmax(max(0, p_a - q_a) / E)
     with q_k = 0, or argmax(p_a / E) when that residual is all zero,
-    E_i = max(-log U_i, 1e-10), U_i = ((Philox(i, b ^ off_hi, off_lo, 2).c0 >> 8) + 1) 2^-24.
+    E_i = max(-log U_i, 1e-10), U_i = ((W_i >> 8) + 1) 2^-24 with W_i = element_words of i with
+    counter (i // 4, b ^ off_hi, off_lo, 2).
     """
     draft = np.asarray(draft, dtype=np.float32)
     target = np.asarray(target, dtype=np.float32)
@@ -194,7 +203,7 @@ def verify_batch(draft, target, tokens, temperatures=None, point_mass=False, see
     qa = qpad[rows, accepted]
     r = np.maximum(pa - qa, np.float32(0))
     cols = np.broadcast_to(np.arange(V, dtype=np.uint32)[None, :], (B, V))
-    w2 = _philox_word0(cols, np.broadcast_to(bb[:, None], (B, V)), np.full((B, V), off_lo, np.uint32),
+    w2 = element_words(cols, np.broadcast_to(bb[:, None], (B, V)), np.full((B, V), off_lo, np.uint32),
                        np.full((B, V), 2, np.uint32), seed)
     U = ((w2 >> np.uint32(8)).astype(np.float32) + np.float32(1)) * np.float32(1.0 / 16777216.0)
     E = np.maximum(-np.log(U), np.float32(1e-10)).astype(np.float32)

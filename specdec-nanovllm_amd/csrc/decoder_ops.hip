@@ -229,8 +229,9 @@ __device__ __forceinline__ bool better(float k, int i, float bk, int bi) {
 // One workgroup per row. Greedy: argmax of the logits. Sampled (T > 0): the
 // reference's argmax(softmax(l / T) / E) with E ~ Exp(1) is the argmax of
 // l / T - log(E) (log is monotone and the softmax normaliser is common to the
-// row), so one pass suffices. E = -log(U), U uniform in (0, 1] from Philox
-// with key = seed and counter = (column, row, offset).
+// row), so one pass suffices. E = -log(U), U uniform in (0, 1] from word
+// (column % 4) of the Philox block with key = seed and counter = (column / 4,
+// row, offset): a thread takes four consecutive columns per Philox call.
 __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) {
   __shared__ float sk[kSampleThreads / 64];
   __shared__ int si[kSampleThreads / 64];
@@ -249,18 +250,22 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) 
   }
   float bk = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < p.V; i += kSampleThreads) {
-    float key = logit_at(p, row, i);
-    if (!greedy) {
-      uint32_t c[4] = {static_cast<uint32_t>(i), static_cast<uint32_t>(row) ^ off1, off0, 0u};
-      sd::philox(c, k0, k1);
-      const float u = (static_cast<float>(c[0] >> 8) + 1.f) * (1.f / 16777216.f);  // (0, 1]
-      const float e = fmaxf(-logf(u), 1e-10f);
-      key = key * inv_t - logf(e);
-    }
-    if (better(key, i, bk, bi)) {
-      bk = key;
-      bi = i;
+  for (int g = threadIdx.x; 4 * g < p.V; g += kSampleThreads) {
+    uint32_t c[4] = {static_cast<uint32_t>(g), static_cast<uint32_t>(row) ^ off1, off0, 0u};
+    if (!greedy) sd::philox(c, k0, k1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 4 * g + e;
+      if (i >= p.V) break;
+      float key = logit_at(p, row, i);
+      if (!greedy) {
+        const float u = (static_cast<float>(c[e] >> 8) + 1.f) * (1.f / 16777216.f);  // (0, 1]
+        key = key * inv_t - logf(fmaxf(-logf(u), 1e-10f));
+      }
+      if (better(key, i, bk, bi)) {
+        bk = key;
+        bi = i;
+      }
     }
   }
 #pragma unroll

@@ -12,14 +12,18 @@
 // Three launches, no host sync:
 //   stats_kernel   (m, l) of x / T over V slices, every row of every sequence
 //                  (draft rows 0..k-1, target rows 0..k), one workgroup per
-//                  (row, slice): HBM-bound, reads every logit once;
-//   resid_kernel   per (sequence, slice): merges the row statistics, redoes
-//                  the k acceptance tests (2k gathered logits), then scans its
-//                  slice of the chosen rows for the residual race;
+//                  (row, slice of 8192 logits): HBM-bound, reads every logit
+//                  once, and records the logit of the row's candidate token;
+//   resid_kernel   per (sequence, slice of 2048 logits): merges the row
+//                  statistics and runs the k acceptance tests on the recorded
+//                  logits (every workgroup of the sequence; a separate launch
+//                  cost more), then the residual race over its slice of the
+//                  accepted position's rows;
 //   finish_kernel  per sequence: merges the slices' races into the bonus.
 // Noise: Philox4x32-10 keyed by rng_state[0]; u_j uses counter (j, b ^ off_hi,
 // off_lo, 1), u_j = (c0 >> 8) 2^-24 in [0, 1); the bonus noise of element i
-// uses (i, b ^ off_hi, off_lo, 2), E = max(-log U, 1e-10), U = ((c0 >> 8) + 1)
+// is word i % 4 of the block with counter (i / 4, b ^ off_hi, off_lo, 2) (one
+// Philox call per four elements), E = max(-log U, 1e-10), U = ((w >> 8) + 1)
 // 2^-24 in (0, 1].
 #include <math.h>
 
@@ -50,6 +54,8 @@ struct VerifyParams {
   int32_t nsplit2;  // V slices of the residual race
   float2* stats;  // [B][2k + 1][nsplit] (m, l) of x / T
   float* part;    // [B][nsplit2][5] residual sum, key_r, idx_r, key_p, idx_p
+  float* gath;    // [B][2k]: logit of candidate x_j in draft row j (slot j) and
+                  // target row j (slot k + j), recorded by the statistics pass
   int64_t* accepted;
   int64_t* bonus;
   uint8_t* mask;  // (B, k)
@@ -119,17 +125,21 @@ __device__ __forceinline__ void slice_of(int V, int nsplit, int split, int& v0, 
 
 // (max, sum exp) of row[v0, v1) / T for this thread's elements: groups of
 // loads issued together, their maximum, then independent exponentials.
+// `want` (or -1): the element whose raw logit is stored to *got by the thread
+// that loads it.
 template <int DT>
 __device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, float T, bool vec4,
-                                          float& m, float& l) {
+                                          int64_t want, float* got, float& m, float& l) {
   if (vec4) {
-    for (int i0 = v0 + 4 * threadIdx.x; i0 < v1; i0 += 16 * kThreads) {
-      float xs[4][4];
+    constexpr int kG = 8;  // 4-element loads a thread has in flight
+    for (int i0 = v0 + 4 * threadIdx.x; i0 < v1; i0 += 4 * kG * kThreads) {
+      float xs[kG][4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kG; ++u) {
         const int i = i0 + 4 * kThreads * u;
         if (i < v1) {
           row.at4(i, xs[u]);
+          if (want >= i && want < i + 4) *got = xs[u][want - i];
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e) xs[u][e] = -INFINITY;
@@ -137,7 +147,7 @@ __device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, fl
       }
       float gm = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < kG; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           xs[u][e] = xs[u][e] / T;
@@ -146,7 +156,7 @@ __device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, fl
       if (gm == -INFINITY) continue;
       float gl = 0.f;
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < kG; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e) gl += expf(xs[u][e] - gm);
       merge_ml(m, l, gm, gl);
@@ -157,7 +167,12 @@ __device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, fl
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int i = i0 + u * kThreads;
-        xs[u] = i < v1 ? row.at(i) / T : -INFINITY;
+        xs[u] = -INFINITY;
+        if (i < v1) {
+          const float x = row.at(i);
+          if (i == want) *got = x;
+          xs[u] = x / T;
+        }
       }
       float gm = xs[0];
 #pragma unroll
@@ -182,10 +197,15 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(VerifyParams p) {
   int v0, v1;
   slice_of(p.V, p.nsplit, split, v0, v1);
   float m = -INFINITY, l = 0.f;
+  // the candidate token of this row: x_r (draft row r) or x_{r-k} (target row
+  // r - k < k); the bonus row k has none
+  const int j = r < p.k ? r : r - p.k;
+  const int64_t want = j < p.k ? p.tokens[b * p.tok_sb + j] : -1;
+  float* got = p.gath + static_cast<int64_t>(b) * 2 * p.k + (r < p.k ? j : p.k + j);
   if (r < p.k)
-    row_stats(draft_row<DDT>(p, b, r), v0, v1, T, p.vec4, m, l);
+    row_stats(draft_row<DDT>(p, b, r), v0, v1, T, p.vec4, want, got, m, l);
   else
-    row_stats(target_row<TDT>(p, b, r - p.k), v0, v1, T, p.vec4, m, l);
+    row_stats(target_row<TDT>(p, b, r - p.k), v0, v1, T, p.vec4, want, got, m, l);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) merge_ml(m, l, __shfl_xor(m, off), __shfl_xor(l, off));
   const int wave = threadIdx.x >> 6;
@@ -239,14 +259,16 @@ struct Race {
   }
 };
 
-template <int DDT, int TDT>
-__global__ __launch_bounds__(kThreads) void resid_kernel(VerifyParams p) {
+// Acceptance of sequence b, run by every race workgroup of the sequence (a
+// separate launch costs more than the repeat): merges the row statistics, runs
+// the k tests on the logits the statistics pass recorded, and returns the
+// accepted length and the (m, l) of target row a and draft row a; workgroup
+// `writer` also stores accepted / mask.
+template <int DDT>
+__device__ int accept(const VerifyParams& p, int b, bool writer, float4& rec) {
   __shared__ float rm[2 * kMaxK + 1], rz[2 * kMaxK + 1];
-  __shared__ int acc_s;
-  __shared__ float red[kThreads / 64][5];
   __shared__ float2 parts[kMaxParts];
-  const int split = static_cast<int>(blockIdx.x % p.nsplit2);
-  const int b = static_cast<int>(blockIdx.x / p.nsplit2);
+  __shared__ int acc_s;
   const int rows = 2 * p.k + 1;
   const float T = temperature(p, b);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -273,8 +295,8 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(VerifyParams p) {
     }
   }
   __syncthreads();
-  // ---- acceptance: lane j of wave 0 tests candidate j (every workgroup of the
-  //      sequence does the same); the first failing lane is the accepted length
+  // ---- acceptance: lane j of wave 0 tests candidate j; the first failing lane
+  //      is the accepted length
   if (wave == 0) {
     bool ok = true;
     const int j = lane;
@@ -282,55 +304,74 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(VerifyParams p) {
       const int64_t x = p.tokens[b * p.tok_sb + j];
       float q = 0.f, pt = 0.f;
       if (x >= 0 && x < p.V) {
-        const float dv = draft_row<DDT>(p, b, j).at(x);
+        const float* g = p.gath + static_cast<int64_t>(b) * 2 * p.k;
+        // point-mass drafts skip the statistics pass: their value is read here
+        const float dv = p.point_mass ? draft_row<DDT>(p, b, j).at(x) : g[j];
         q = p.point_mass ? dv : expf(dv / T - rm[j]) / rz[j];
-        pt = expf(target_row<TDT>(p, b, j).at(x) / T - rm[p.k + j]) / rz[p.k + j];
+        pt = expf(g[p.k + j] / T - rm[p.k + j]) / rz[p.k + j];
       }
       const float ratio = q > 0.f ? fminf(pt / fmaxf(q, 1e-10f), 1.f) : 0.f;
       uint32_t c[4];
       philox_words(p, static_cast<uint32_t>(j), b, 1u, c);
       const float u = static_cast<float>(c[0] >> 8) * (1.f / 16777216.f);  // [0, 1)
       ok = u < ratio;
-      if (split == 0) p.mask[static_cast<int64_t>(b) * p.k + j] = ok ? 1 : 0;
+      if (writer) p.mask[static_cast<int64_t>(b) * p.k + j] = ok ? 1 : 0;
     }
     const unsigned long long fails = __ballot(!ok);
     const int a = fails ? __ffsll(static_cast<long long>(fails)) - 1 : p.k;
     if (lane == 0) {
       acc_s = a;
-      if (split == 0) p.accepted[b] = a;
+      if (writer) p.accepted[b] = a;
     }
   }
   __syncthreads();
   const int a = acc_s;
+  // (m, l) of target row a and of draft row a (unused when a == k)
+  rec = make_float4(rm[p.k + a], rz[p.k + a], a < p.k ? rm[a] : 0.f, a < p.k ? rz[a] : 1.f);
+  return a;
+}
+
+
+// Residual race over one slice of the accepted position's rows.
+template <int DDT, int TDT>
+__global__ __launch_bounds__(kThreads) void resid_kernel(VerifyParams p) {
+  __shared__ float red[kThreads / 64][5];
+  const int split = static_cast<int>(blockIdx.x % p.nsplit2);
+  const int b = static_cast<int>(blockIdx.x / p.nsplit2);
+  const float T = temperature(p, b);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float4 rc;
+  const int a = accept<DDT>(p, b, split == 0, rc);
   // ---- residual race over this slice: max(0, p_a - q_a) / E and p_a / E
-  const int rp = p.k + a;
   const bool has_q = a < p.k;
   const Row<TDT> prow = target_row<TDT>(p, b, a);
   const Row<DDT> qrow = draft_row<DDT>(p, b, has_q ? a : 0);
-  const float pm = rm[rp], pz = rz[rp];
-  const float qm = has_q ? rm[a] : 0.f, qz = has_q ? rz[a] : 1.f;
+  const float pm = rc.x, pz = rc.y;
+  const float qm = rc.z, qz = rc.w;
   int v0, v1;
   slice_of(p.V, p.nsplit2, split, v0, v1);
   Race race;
-  auto step = [&](int i, float tv, float dv) {
+  // element i's noise is word i % 4 of the Philox block (i / 4, b, offset, 2)
+  auto step = [&](int i, float tv, float dv, uint32_t w) {
     const float pv = expf(tv / T - pm) / pz;
     float qv = 0.f;
     if (has_q) qv = p.point_mass ? dv : expf(dv / T - qm) / qz;
     const float r = fmaxf(pv - qv, 0.f);
     race.rsum += r;
-    uint32_t c[4];
-    philox_words(p, static_cast<uint32_t>(i), b, 2u, c);
-    const float U = (static_cast<float>(c[0] >> 8) + 1.f) * (1.f / 16777216.f);  // (0, 1]
+    const float U = (static_cast<float>(w >> 8) + 1.f) * (1.f / 16777216.f);  // (0, 1]
     const float E = fmaxf(-logf(U), 1e-10f);
     race.take(r / E, i, pv / E, i);
   };
   if (p.vec4) {
+    // slices start at multiples of 4: a 4-element group is one Philox block
     for (int i0 = v0 + 4 * threadIdx.x; i0 < v1; i0 += 4 * kThreads) {
       float ts[4], ds[4] = {0.f, 0.f, 0.f, 0.f};
       prow.at4(i0, ts);
       if (has_q) qrow.at4(i0, ds);
+      uint32_t c[4];
+      philox_words(p, static_cast<uint32_t>(i0 >> 2), b, 2u, c);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) step(i0 + e, ts[e], ds[e]);
+      for (int e = 0; e < 4; ++e) step(i0 + e, ts[e], ds[e], c[e]);
     }
   } else {
     for (int i0 = v0 + threadIdx.x; i0 < v1; i0 += kThreads * kUnroll) {
@@ -345,7 +386,9 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(VerifyParams p) {
       for (int u = 0; u < kUnroll; ++u) {
         const int i = i0 + u * kThreads;
         if (i >= v1) break;
-        step(i, ts[u], ds[u]);
+        uint32_t c[4];
+        philox_words(p, static_cast<uint32_t>(i >> 2), b, 2u, c);
+        step(i, ts[u], ds[u], c[i & 3]);
       }
     }
   }
@@ -387,24 +430,28 @@ __global__ __launch_bounds__(64) void finish_kernel(VerifyParams p) {
   }
 }
 
-// Slices of the row statistics: ~8192 logits per workgroup (two rounds of
-// four 4-element loads per thread), at most kMaxParts (row, slice) partials
-// per sequence.
+// Slices of the row statistics: ~8192 logits per workgroup (one round of
+// eight 4-element loads per thread; 32K-logit slices were slower), at most
+// kMaxParts (row, slice) partials per sequence.
 int nsplit_for(int32_t V, int32_t k) {
   const int cap = kMaxParts / (2 * k + 1);
   const int n = (V + 8191) / 8192;
   return n < 1 ? 1 : (n > cap ? cap : n);
 }
 
-// Slices of the residual race: ~1024 logits per workgroup (4 per thread), so
+// Slices of the residual race: ~2048 logits per workgroup (8 per thread), so
 // the per-element work (Philox, log, exp, divides) spreads over many waves.
 int nsplit2_for(int32_t V) {
-  const int n = (V + 1023) / 1024;
+  const int n = (V + 2047) / 2048;
   return n < 1 ? 1 : (n > 1024 ? 1024 : n);
 }
 
 size_t stats_bytes(int64_t B, int32_t k, int ns) {
   return (static_cast<size_t>(B) * (2 * k + 1) * ns * sizeof(float2) + 255) / 256 * 256;
+}
+
+size_t parts_bytes(int64_t B, int ns2) {
+  return (static_cast<size_t>(B) * ns2 * 5 * sizeof(float) + 255) / 256 * 256;
 }
 
 template <int DDT, int TDT>
@@ -432,7 +479,8 @@ void launch_pair(int32_t ddt, int32_t tdt, const VerifyParams& p, dim3 g1, dim3 
 extern "C" size_t sd_verify_batch_workspace_size(int64_t batch, int32_t k, int32_t vocab) {
   if (batch <= 0 || k <= 0 || vocab <= 0) return 0;
   const int ns = nsplit_for(vocab, k);
-  return stats_bytes(batch, k, ns) + static_cast<size_t>(batch) * nsplit2_for(vocab) * 5 * sizeof(float);
+  return stats_bytes(batch, k, ns) + parts_bytes(batch, nsplit2_for(vocab)) +
+         (static_cast<size_t>(batch) * 2 * k * sizeof(float) + 255) / 256 * 256;
 }
 
 extern "C" int sd_verify_batch(const void* draft, int64_t draft_stride_b, int64_t draft_stride_k,
@@ -497,6 +545,8 @@ extern "C" int sd_verify_batch(const void* draft, int64_t draft_stride_b, int64_
            rows_aligned(target, target_dtype, target_stride_b, target_stride_k);
   p.stats = static_cast<float2*>(workspace);
   p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + stats_bytes(batch, k, ns));
+  p.gath = reinterpret_cast<float*>(static_cast<char*>(workspace) + stats_bytes(batch, k, ns) +
+                                    parts_bytes(batch, ns2));
   p.accepted = accepted;
   p.bonus = bonus;
   p.mask = accept_mask;
@@ -504,7 +554,7 @@ extern "C" int sd_verify_batch(const void* draft, int64_t draft_stride_b, int64_
   const unsigned nb = static_cast<unsigned>(batch * ns);
   launch_pair(draft_dtype, target_dtype, p, dim3(nb, 2 * k + 1),
               dim3(static_cast<unsigned>(batch * ns2)), st);
-  int rc = sd::check_launch("verify_batch statistics / residual");
+  int rc = sd::check_launch("verify_batch statistics / acceptance / residual");
   if (rc != SD_OK) return rc;
   hipLaunchKernelGGL(finish_kernel, dim3(static_cast<unsigned>(batch)), dim3(64), 0, st, p);
   return sd::check_launch("verify_batch finish");
