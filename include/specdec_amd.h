@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define SD_ABI_VERSION 1
+#define SD_ABI_VERSION 2
 
 typedef enum sd_status {
   SD_OK = 0,
@@ -275,10 +275,14 @@ int sd_silu_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride, 
  *   rng_state[1], 0).
  *   rng_state: (2,) int64 on the device, read only; the caller advances the
  *   offset between calls (on the stream, so graph replays advance it too).
+ * Two launches: each row split over 4096-column workgroups, then a per-row
+ * merge of their (key, column) partials held in the workspace
+ * (sd_sample_workspace_size bytes, 8-byte aligned). rows <= 65535.
  */
+size_t sd_sample_workspace_size(int64_t rows, int32_t vocab);
 int sd_sample(const void* logits, int64_t logits_stride, int32_t dtype, int64_t rows,
               int32_t vocab, const float* temperatures, const int64_t* rng_state,
-              int64_t* out_tokens, void* stream);
+              int64_t* out_tokens, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Variable-length causal attention, the prefill branch of the attention layer:

@@ -16,7 +16,7 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libspecdec_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 SD_OK, SD_ERR_VALUE, SD_ERR_UNSUPPORTED, SD_ERR_WORKSPACE, SD_ERR_HIP = range(5)
 SD_BF16, SD_F16, SD_F32 = 0, 1, 2
@@ -68,9 +68,11 @@ SIGNATURES.update({
         _p, _p, _i64, _i64,             # positions, cos_sin, stride, max_position
         _i32, _p]),                     # dtype, stream
     "sd_silu_mul": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i32, _i32, _p]),
+    "sd_sample_workspace_size": (ctypes.c_size_t, [_i64, _i32]),
     "sd_sample": (ctypes.c_int, [
         _p, _i64, _i32, _i64, _i32,     # logits, stride, dtype, rows, vocab
-        _p, _p, _p, _p]),               # temperatures, rng_state, out_tokens, stream
+        _p, _p, _p,                     # temperatures, rng_state, out_tokens
+        _p, ctypes.c_size_t, _p]),      # workspace, bytes, stream
     "sd_quantize_int8": (ctypes.c_int, [
         _p, _i64, _i32, _p, _i64,       # w, stride, dtype, q, stride
         _p, _i64, _i32, _i32, _p]),     # scale, N, K, group_size, stream

@@ -7,9 +7,11 @@
 //   qk_norm_rope_kernel  per-head q/k RMSNorm then rotate-half RoPE, in place
 //                        (models/qwen3.py:80-88, layers/rotary_embedding.py:6-48)
 //   silu_mul_kernel      SiluAndMul (layers/activation.py:6-11)
-//   sample_kernel        Sampler: temperature + exponential-race (Gumbel-max)
+//   sample_partial_kernel / sample_merge_kernel
+//                        Sampler: temperature + exponential-race (Gumbel-max)
 //                        sampling, or greedy argmax (layers/sampler.py:6-12,
-//                        spec_decode/draft_proposer.py:505-510)
+//                        spec_decode/draft_proposer.py:505-510), a row split
+//                        over 4096-column workgroups and merged per row
 //
 // Rounding follows the modules' eager torch semantics: fp32 arithmetic, a
 // 16-bit rounding wherever the module converts back to the activation dtype
@@ -210,9 +212,13 @@ struct SampleParams {
   const float* temp;      // (rows,), NULL: greedy
   const int64_t* state;   // (2,) device: seed, offset; read only
   int64_t* out;
+  float2* part;           // [rows][nslices] (best key, its index as int bits)
+  int32_t nslices;
 };
 
-constexpr int kSampleThreads = 1024;
+constexpr int kSampleThreads = 256;
+constexpr int kSampleGroups = 4;  // 4-column groups per thread per slice
+constexpr int kSampleSlice = 4 * kSampleGroups * kSampleThreads;  // 4096 columns
 
 __device__ __forceinline__ float logit_at(const SampleParams& p, int64_t row, int i) {
   if (p.dtype == SD_F32) return static_cast<const float*>(p.logits)[row * p.ls + i];
@@ -226,19 +232,34 @@ __device__ __forceinline__ bool better(float k, int i, float bk, int bi) {
   return k > bk || (k == bk && i < bi);
 }
 
-// One workgroup per row. Greedy: argmax of the logits. Sampled (T > 0): the
-// reference's argmax(softmax(l / T) / E) with E ~ Exp(1) is the argmax of
-// l / T - log(E) (log is monotone and the softmax normaliser is common to the
-// row), so one pass suffices. E = -log(U), U uniform in (0, 1] from word
-// (column % 4) of the Philox block with key = seed and counter = (column / 4,
-// row, offset): a thread takes four consecutive columns per Philox call.
-__global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) {
+__device__ __forceinline__ void wave_best(float& bk, int& bi) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ok = __shfl_xor(bk, off);
+    const int oi = __shfl_xor(bi, off);
+    if (better(ok, oi, bk, bi)) {
+      bk = ok;
+      bi = oi;
+    }
+  }
+}
+
+// Greedy: argmax of the logits. Sampled (T > 0): the reference's
+// argmax(softmax(l / T) / E) with E ~ Exp(1) is the argmax of l / T - log(E)
+// (log is monotone and the softmax normaliser is common to the row), so one
+// pass suffices; the keys are scaled by log2(e) (same argmax). E = -log(U), U
+// uniform in (0, 1] from word (column % 4) of the Philox block with key = seed
+// and counter = (column / 4, row, offset): a thread takes four consecutive
+// columns per Philox call.
+// Pass 1, grid (slice, row): the best (key, column) of a 4096-column slice.
+__global__ __launch_bounds__(kSampleThreads) void sample_partial_kernel(SampleParams p) {
   __shared__ float sk[kSampleThreads / 64];
   __shared__ int si[kSampleThreads / 64];
-  const int64_t row = blockIdx.x;
+  const int64_t row = blockIdx.y;
   const float T = p.temp ? p.temp[row] : 0.f;
   const bool greedy = !(T > 0.f);
-  const float inv_t = greedy ? 1.f : 1.f / T;
+  // keys scaled by log2(e) (the argmax is the same): l log2(e) / T - log2(E)
+  const float s2 = greedy ? 1.f : 1.4426950408889634f / T;
   uint32_t k0 = 0, k1 = 0, off0 = 0, off1 = 0;
   if (!greedy) {
     const uint64_t seed = static_cast<uint64_t>(p.state[0]);
@@ -250,7 +271,11 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) 
   }
   float bk = -INFINITY;
   int bi = 0x7fffffff;
-  for (int g = threadIdx.x; 4 * g < p.V; g += kSampleThreads) {
+  const int g0 = blockIdx.x * (kSampleSlice / 4);
+#pragma unroll
+  for (int j = 0; j < kSampleGroups; ++j) {
+    const int g = g0 + j * kSampleThreads + threadIdx.x;
+    if (4 * g >= p.V) break;
     uint32_t c[4] = {static_cast<uint32_t>(g), static_cast<uint32_t>(row) ^ off1, off0, 0u};
     if (!greedy) sd::philox(c, k0, k1);
 #pragma unroll
@@ -260,7 +285,9 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) 
       float key = logit_at(p, row, i);
       if (!greedy) {
         const float u = (static_cast<float>(c[e] >> 8) + 1.f) * (1.f / 16777216.f);  // (0, 1]
-        key = key * inv_t - logf(fmaxf(-logf(u), 1e-10f));
+        // E = max(-ln u, 1e-10); native log2 (v_log_f32)
+        const float E = fmaxf(-__builtin_amdgcn_logf(u) * 0.6931471805599453f, 1e-10f);
+        key = key * s2 - __builtin_amdgcn_logf(E);
       }
       if (better(key, i, bk, bi)) {
         bk = key;
@@ -268,15 +295,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) 
       }
     }
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ok = __shfl_xor(bk, off);
-    const int oi = __shfl_xor(bi, off);
-    if (better(ok, oi, bk, bi)) {
-      bk = ok;
-      bi = oi;
-    }
-  }
+  wave_best(bk, bi);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (lane == 0) {
     sk[wave] = bk;
@@ -289,9 +308,27 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) 
         bk = sk[w];
         bi = si[w];
       }
-    p.out[row] = bi == 0x7fffffff ? 0 : bi;  // an all-NaN row gives token 0
+    p.part[row * p.nslices + blockIdx.x] = make_float2(bk, __int_as_float(bi));
   }
 }
+
+// Pass 2, one wave per row: the best of the row's slices.
+__global__ __launch_bounds__(64) void sample_merge_kernel(SampleParams p) {
+  const int64_t row = blockIdx.x;
+  float bk = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int s = threadIdx.x; s < p.nslices; s += 64) {
+    const float2 v = p.part[row * p.nslices + s];
+    if (better(v.x, __float_as_int(v.y), bk, bi)) {
+      bk = v.x;
+      bi = __float_as_int(v.y);
+    }
+  }
+  wave_best(bk, bi);
+  if (threadIdx.x == 0) p.out[row] = bi == 0x7fffffff ? 0 : bi;  // an all-NaN row gives token 0
+}
+
+int sample_slices(int32_t vocab) { return (vocab + kSampleSlice - 1) / kSampleSlice; }
 
 bool is16(int32_t dtype) { return dtype == SD_BF16 || dtype == SD_F16; }
 
@@ -405,9 +442,15 @@ extern "C" int sd_silu_mul(const void* x, int64_t x_stride, void* out, int64_t o
   return sd::check_launch("silu_mul");
 }
 
+extern "C" size_t sd_sample_workspace_size(int64_t rows, int32_t vocab) {
+  if (rows <= 0 || vocab <= 0) return 0;
+  return static_cast<size_t>(rows) * sample_slices(vocab) * sizeof(float2);
+}
+
 extern "C" int sd_sample(const void* logits, int64_t logits_stride, int32_t dtype, int64_t rows,
                          int32_t vocab, const float* temperatures, const int64_t* rng_state,
-                         int64_t* out_tokens, void* stream) {
+                         int64_t* out_tokens, void* workspace, size_t workspace_bytes,
+                         void* stream) {
   sd::clear_error();
   if (rows < 0 || vocab <= 0 || (dtype != SD_BF16 && dtype != SD_F16 && dtype != SD_F32)) {
     sd::set_error("sample: vocab must be positive, logits bf16/fp16/fp32 (vocab=%d dtype=%d)",
@@ -419,12 +462,24 @@ extern "C" int sd_sample(const void* logits, int64_t logits_stride, int32_t dtyp
     sd::set_error("sample: null pointer argument (temperatures need rng_state)");
     return SD_ERR_VALUE;
   }
-  if (rows > 0x7fffffff) {
-    sd::set_error("sample: too many rows (%lld)", (long long)rows);
+  if (rows > 65535) {
+    sd::set_error("sample: at most 65535 rows per call (%lld)", (long long)rows);
     return SD_ERR_UNSUPPORTED;
   }
-  SampleParams p{logits, logits_stride, dtype, vocab, temperatures, rng_state, out_tokens};
-  hipLaunchKernelGGL(sample_kernel, dim3(static_cast<unsigned>(rows)), dim3(kSampleThreads), 0,
-                     static_cast<hipStream_t>(stream), p);
-  return sd::check_launch("sample");
+  const size_t need = sd_sample_workspace_size(rows, vocab);
+  if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 7u)) {
+    sd::set_error("sample: workspace of %zu bytes (8-byte aligned) required, got %zu", need,
+                  workspace ? workspace_bytes : (size_t)0);
+    return SD_ERR_WORKSPACE;
+  }
+  SampleParams p{logits, logits_stride, dtype, vocab, temperatures, rng_state, out_tokens,
+                 static_cast<float2*>(workspace), sample_slices(vocab)};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(sample_partial_kernel,
+                     dim3(static_cast<unsigned>(p.nslices), static_cast<unsigned>(rows)),
+                     dim3(kSampleThreads), 0, st, p);
+  const int rc = sd::check_launch("sample (slices)");
+  if (rc != SD_OK) return rc;
+  hipLaunchKernelGGL(sample_merge_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, st, p);
+  return sd::check_launch("sample (merge)");
 }

@@ -10,8 +10,9 @@
 //   to 0, drawn as argmax(resid / E), E ~ Exp(1) (verify.py:171-183,203-209).
 //
 // Three launches, no host sync:
-//   stats_kernel   (m, l) of x / T over V slices, every row of every sequence
-//                  (draft rows 0..k-1, target rows 0..k), one workgroup per
+//   stats_kernel   (m, l) of x log2(e) / T (exp2 domain) over V slices, every
+//                  row of every sequence (draft rows 0..k-1, target rows
+//                  0..k), one workgroup per
 //                  (row, slice of 8192 logits): HBM-bound, reads every logit
 //                  once, and records the logit of the row's candidate token;
 //   resid_kernel   per (sequence, slice of 2048 logits): merges the row
@@ -52,7 +53,7 @@ struct VerifyParams {
   int32_t vec4;     // every row starts 4-element aligned and V % 4 == 0
   int32_t nsplit;   // V slices of the row statistics
   int32_t nsplit2;  // V slices of the residual race
-  float2* stats;  // [B][2k + 1][nsplit] (m, l) of x / T
+  float2* stats;  // [B][2k + 1][nsplit] (m, l) of x log2(e) / T, l = sum 2^(x' - m)
   float* part;    // [B][nsplit2][5] residual sum, key_r, idx_r, key_p, idx_p
   float* gath;    // [B][2k]: logit of candidate x_j in draft row j (slot j) and
                   // target row j (slot k + j), recorded by the statistics pass
@@ -110,7 +111,7 @@ __device__ __forceinline__ float temperature(const VerifyParams& p, int b) {
 __device__ __forceinline__ void merge_ml(float& m, float& l, float m2, float l2) {
   const float M = fmaxf(m, m2);
   if (M == -INFINITY) return;
-  l = l * expf(m - M) + l2 * expf(m2 - M);
+  l = l * sd::fast_exp2(m - M) + l2 * sd::fast_exp2(m2 - M);
   m = M;
 }
 
@@ -123,12 +124,13 @@ __device__ __forceinline__ void slice_of(int V, int nsplit, int split, int& v0, 
   v1 = static_cast<int>(e < V ? e : V);
 }
 
-// (max, sum exp) of row[v0, v1) / T for this thread's elements: groups of
+// (max, sum 2^) of row[v0, v1) * s2 (s2 = log2(e) / T) for this thread's
+// elements, in the exp2 domain (a multiply and a native exp2 per logit): groups of
 // loads issued together, their maximum, then independent exponentials.
 // `want` (or -1): the element whose raw logit is stored to *got by the thread
 // that loads it.
 template <int DT>
-__device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, float T, bool vec4,
+__device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, float s2, bool vec4,
                                           int64_t want, float* got, float& m, float& l) {
   if (vec4) {
     constexpr int kG = 8;  // 4-element loads a thread has in flight
@@ -150,7 +152,7 @@ __device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, fl
       for (int u = 0; u < kG; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          xs[u][e] = xs[u][e] / T;
+          xs[u][e] = xs[u][e] * s2;
           gm = fmaxf(gm, xs[u][e]);
         }
       if (gm == -INFINITY) continue;
@@ -158,7 +160,7 @@ __device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, fl
 #pragma unroll
       for (int u = 0; u < kG; ++u)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) gl += expf(xs[u][e] - gm);
+        for (int e = 0; e < 4; ++e) gl += sd::fast_exp2(xs[u][e] - gm);
       merge_ml(m, l, gm, gl);
     }
   } else {
@@ -171,7 +173,7 @@ __device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, fl
         if (i < v1) {
           const float x = row.at(i);
           if (i == want) *got = x;
-          xs[u] = x / T;
+          xs[u] = x * s2;
         }
       }
       float gm = xs[0];
@@ -180,7 +182,7 @@ __device__ __forceinline__ void row_stats(const Row<DT>& row, int v0, int v1, fl
       if (gm == -INFINITY) continue;
       float gl = 0.f;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) gl += expf(xs[u] - gm);
+      for (int u = 0; u < kUnroll; ++u) gl += sd::fast_exp2(xs[u] - gm);
       merge_ml(m, l, gm, gl);
     }
   }
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(VerifyParams p) {
   const int b = static_cast<int>(blockIdx.x / p.nsplit);
   const int r = blockIdx.y;
   if (p.point_mass && r < p.k) return;  // probabilities already: no statistics
-  const float T = temperature(p, b);
+  const float s2 = 1.4426950408889634f / temperature(p, b);  // log2(e) / T
   int v0, v1;
   slice_of(p.V, p.nsplit, split, v0, v1);
   float m = -INFINITY, l = 0.f;
@@ -203,9 +205,9 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(VerifyParams p) {
   const int64_t want = j < p.k ? p.tokens[b * p.tok_sb + j] : -1;
   float* got = p.gath + static_cast<int64_t>(b) * 2 * p.k + (r < p.k ? j : p.k + j);
   if (r < p.k)
-    row_stats(draft_row<DDT>(p, b, r), v0, v1, T, p.vec4, want, got, m, l);
+    row_stats(draft_row<DDT>(p, b, r), v0, v1, s2, p.vec4, want, got, m, l);
   else
-    row_stats(target_row<TDT>(p, b, r - p.k), v0, v1, T, p.vec4, want, got, m, l);
+    row_stats(target_row<TDT>(p, b, r - p.k), v0, v1, s2, p.vec4, want, got, m, l);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) merge_ml(m, l, __shfl_xor(m, off), __shfl_xor(l, off));
   const int wave = threadIdx.x >> 6;
@@ -270,7 +272,7 @@ __device__ int accept(const VerifyParams& p, int b, bool writer, float4& rec) {
   __shared__ float2 parts[kMaxParts];
   __shared__ int acc_s;
   const int rows = 2 * p.k + 1;
-  const float T = temperature(p, b);
+  const float s2 = 1.4426950408889634f / temperature(p, b);  // log2(e) / T
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // ---- row statistics: every (row, slice) partial loaded in one round, then
   //      one wave per row merges its slices
@@ -307,8 +309,8 @@ __device__ int accept(const VerifyParams& p, int b, bool writer, float4& rec) {
         const float* g = p.gath + static_cast<int64_t>(b) * 2 * p.k;
         // point-mass drafts skip the statistics pass: their value is read here
         const float dv = p.point_mass ? draft_row<DDT>(p, b, j).at(x) : g[j];
-        q = p.point_mass ? dv : expf(dv / T - rm[j]) / rz[j];
-        pt = expf(g[p.k + j] / T - rm[p.k + j]) / rz[p.k + j];
+        q = p.point_mass ? dv : sd::fast_exp2(dv * s2 - rm[j]) / rz[j];
+        pt = sd::fast_exp2(g[p.k + j] * s2 - rm[p.k + j]) / rz[p.k + j];
       }
       const float ratio = q > 0.f ? fminf(pt / fmaxf(q, 1e-10f), 1.f) : 0.f;
       uint32_t c[4];
@@ -338,7 +340,7 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(VerifyParams p) {
   __shared__ float red[kThreads / 64][5];
   const int split = static_cast<int>(blockIdx.x % p.nsplit2);
   const int b = static_cast<int>(blockIdx.x / p.nsplit2);
-  const float T = temperature(p, b);
+  const float s2 = 1.4426950408889634f / temperature(p, b);  // log2(e) / T
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float4 rc;
   const int a = accept<DDT>(p, b, split == 0, rc);
@@ -353,13 +355,13 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(VerifyParams p) {
   Race race;
   // element i's noise is word i % 4 of the Philox block (i / 4, b, offset, 2)
   auto step = [&](int i, float tv, float dv, uint32_t w) {
-    const float pv = expf(tv / T - pm) / pz;
+    const float pv = sd::fast_exp2(tv * s2 - pm) / pz;
     float qv = 0.f;
-    if (has_q) qv = p.point_mass ? dv : expf(dv / T - qm) / qz;
+    if (has_q) qv = p.point_mass ? dv : sd::fast_exp2(dv * s2 - qm) / qz;
     const float r = fmaxf(pv - qv, 0.f);
     race.rsum += r;
     const float U = (static_cast<float>(w >> 8) + 1.f) * (1.f / 16777216.f);  // (0, 1]
-    const float E = fmaxf(-logf(U), 1e-10f);
+    const float E = fmaxf(-__builtin_amdgcn_logf(U) * 0.6931471805599453f, 1e-10f);  // -ln U
     race.take(r / E, i, pv / E, i);
   };
   if (p.vec4) {

@@ -420,9 +420,11 @@ def sample(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
     if rows:
         lib = _lib.load()
         with torch.cuda.device(dev):
+            ws_bytes = lib.sd_sample_workspace_size(rows, V)
+            ws = _workspace(ws_bytes, dev)
             rc = lib.sd_sample(logits.data_ptr(), logits.stride(0), _lib.dtype_code(logits.dtype),
-                               rows, V, _ptr(t), _ptr(rng_state), o.data_ptr(),
-                               _lib.stream_ptr(dev))
+                               rows, V, _ptr(t), _ptr(rng_state), o.data_ptr(), _ptr(ws),
+                               ws_bytes, _lib.stream_ptr(dev))
         _lib.check(rc)
         if advance:
             rng_state[1:].add_(1)

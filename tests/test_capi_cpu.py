@@ -55,7 +55,7 @@ def test_ctypes_table_matches_header_arity():
 
 def test_abi_version_and_empty_error():
     lib = _lib.load()
-    assert lib.sd_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.sd_abi_version() == _lib.ABI_VERSION == 2
     assert isinstance(lib.sd_last_error(), bytes)
 
 
