@@ -202,6 +202,25 @@ int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t 
                     void* stream);
 
 /*
+ * SiluAndMul fused into the W8A16 linear: y = (bf16(bf16(silu(g)) * u)) @
+ * (w * scale)^T (+ bias) with g = gate_up[m, 0:K] and u = gate_up[m, K:2K],
+ * the MLP's act_fn followed by down_proj (nanovllm/layers/activation.py:6-11,
+ * models/qwen3.py Qwen3MLP.forward). No counterpart entry in the reference:
+ * the fusion saves the SiluAndMul launch and its round trip through memory.
+ * The activation equals sd_silu_mul's output bit for bit, so y equals
+ * sd_silu_mul followed by sd_w8a16_linear. gate_up: (M, >= 2K) dtype, row
+ * stride gate_up_stride_m; the rest as sd_w8a16_linear (no workspace). The
+ * SiLU is computed once per workgroup while its activation rows are staged in
+ * LDS, which holds while min(M, 16) * (2 K + 16) <= 33,024 bytes (M = 1 for
+ * K = 3072); beyond that the result is the same but each wave recomputes the
+ * SiLU of its operands, slower than the two separate calls.
+ */
+int sd_w8a16_silu_linear(const void* gate_up, int64_t gate_up_stride_m, const int8_t* w,
+                         int64_t w_stride_n, const void* scale, int32_t scale_dtype,
+                         int32_t group_size, const void* bias, void* y, int64_t y_stride_m,
+                         int64_t M, int64_t N, int64_t K, int32_t dtype, void* stream);
+
+/*
  * Symmetric int8 weight quantization, the producer of the W8A16 format:
  * `quantize_weight` (nanovllm/layers/quant.py:123-148) and the offline
  * converter's `quantize_tensor` (scripts/quantize_int8.py:53-83). Per row and

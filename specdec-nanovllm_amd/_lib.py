@@ -49,6 +49,11 @@ SIGNATURES = {
         _p, _i64, _i64,                 # out, strides
         _p, _sz, _i32, _p]),            # workspace, bytes, num_splits, stream
     "sd_w8a16_workspace_size": (_sz, [_i64, _i64, _i64, _i32]),
+    "sd_w8a16_silu_linear": (ctypes.c_int, [
+        _p, _i64, _p, _i64,             # gate_up, stride, w, w_stride
+        _p, _i32, _i32, _p,             # scale, scale_dtype, group_size, bias
+        _p, _i64,                       # y, y_stride
+        _i64, _i64, _i64, _i32, _p]),   # M, N, K, dtype, stream
     "sd_w8a16_linear": (ctypes.c_int, [
         _p, _i64, _p, _i64,             # x, x_stride, w, w_stride
         _p, _i32, _i32, _p,             # scale, scale_dtype, group_size, bias

@@ -186,21 +186,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(SiluParams p) {
   const int e0 = static_cast<int>(idx - m * chunks) * 8;
   const sd::u32x4 g = sd::load16(p.x + m * p.xs + e0);
   const sd::u32x4 u = sd::load16(p.x + m * p.xs + p.width + e0);
-  const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float r[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float gv = sd::from_bits<T>(static_cast<uint16_t>(gw[i] >> (16 * h)));
-      const float uv = sd::from_bits<T>(static_cast<uint16_t>(uw[i] >> (16 * h)));
-      const float sv = round16<T>(gv / (1.f + expf(-gv)));
-      r[h] = sv * uv;
-    }
-    o[i] = sd::pack2<T>(r[0], r[1]);
-  }
-  sd::store16(p.out + m * p.os + e0, sd::u32x4{o[0], o[1], o[2], o[3]});
+  sd::store16(p.out + m * p.os + e0, sd::silu_mul8<T>(g, u));
 }
 
 // ------------------------------------------------------------------ sampling

@@ -109,6 +109,30 @@ __device__ __forceinline__ float sum_over_groups(float v) {
 // results below 2^-126 flush to 0, 2^-inf = 0. Softmax weights only.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// SiluAndMul on 8 elements: bf16(bf16(silu(g)) * u) per element (T = the
+// activation type), the eager module's roundings; g and u are 8 packed 16-bit
+// values each. Shared by the SiLU kernel and the W8A16 activation path that
+// fuses it, so both give the same bits.
+template <typename T>
+__device__ __forceinline__ u32x4 silu_mul8(u32x4 g, u32x4 u) {
+#pragma clang fp contract(off)
+  const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float r[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float gv = from_bits<T>(static_cast<uint16_t>(gw[i] >> (16 * h)));
+      const float uv = from_bits<T>(static_cast<uint16_t>(uw[i] >> (16 * h)));
+      const float sv = static_cast<float>(static_cast<T>(gv / (1.f + expf(-gv))));
+      r[h] = sv * uv;
+    }
+    o[i] = pack2<T>(r[0], r[1]);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
 // LDS transpose read (ds_read_b64_tr_b16): within every 16-lane block, lane
 // 4a + c receives 16-bit element c of the 8-byte chunks addressed by lanes
 // a, a + 4, a + 8 and a + 12 of that block, in that order.

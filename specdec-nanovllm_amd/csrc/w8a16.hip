@@ -26,6 +26,8 @@
 // fp16 value 1024 + b + 128, exact; subtracting 1152 (packed fp16) gives b.
 // int8 -> bf16: v_cvt_f32_ubyte of (b ^ 0x80) minus 128 is b as fp32, whose
 // upper half is the exact bf16 (|b| <= 127 needs 7 mantissa bits).
+#include <mutex>
+
 #include "sd_common.h"
 
 namespace {
@@ -53,6 +55,7 @@ struct W8Params {
   int32_t xpitch;  // bytes per activation row in LDS (staged activations only)
   int32_t xbytes;  // XL: bytes of staged activation rows; the scale table follows
   int32_t ngmax;   // XL: most row groups one wave owns
+  int64_t up;      // SL: elements from a gate_up row's gate half to its up half
 };
 
 __device__ __forceinline__ float load_scale(const void* s, int dtype, int64_t i) {
@@ -118,8 +121,12 @@ template <> __device__ __forceinline__ u32x4 dequant8<__bf16>(uint32_t w0, uint3
 // loads were as many instructions per chunk as the weight loads (4 of 64
 // lanes active), and every vector load instruction costs the compute unit's
 // address path the same time whatever its lane count.
+//
+// SL: the activation is SiluAndMul of a gate_up row, bf16(bf16(silu(g)) * u)
+// with g = x[m, k] and u = x[m, up + k], formed where the activation is loaded
+// (the down projection reads the gate_up projection's output directly).
 template <typename T, int MT, int NT, int KW, int U, bool PER_GROUP, bool CONTIG = false,
-          int D = 2, bool XL = false>
+          int D = 2, bool XL = false, bool SL = false>
 __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
   static_assert(U == 2 || U == 4 || U == 8, "a chunk row segment is 64 U bytes");
   constexpr int LPR = 4 * U;         // lanes per row segment (16-byte units per row)
@@ -197,6 +204,10 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
   struct Regs {
     u32x4 w[NLD];
     u32x4 x[XL ? 1 : U][MT][2];  // activation B operands of the chunk's steps (not XL)
+    // SL: the up halves, as loaded; SiluAndMul is applied where the operand is
+    // used (applying it here would wait for these loads, queued behind the
+    // weight prefetch)
+    u32x4 xu[SL && !XL ? U : 1][MT][2];
   };
   // Every call issues the same loads: steps past this wave's K range are
   // clamped into the matrix (loaded, never used), rows past N / M read a valid
@@ -223,9 +234,17 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
         if (xok[mt]) {
           R.x[u][mt][0] = sd::load16(xp[mt] + k0);
           R.x[u][mt][1] = sd::load16(xp[mt] + k0 + 8);
+          if constexpr (SL) {
+            R.xu[u][mt][0] = sd::load16(xp[mt] + p.up + k0);
+            R.xu[u][mt][1] = sd::load16(xp[mt] + p.up + k0 + 8);
+          }
         } else {
           R.x[u][mt][0] = u32x4{0u, 0u, 0u, 0u};
           R.x[u][mt][1] = u32x4{0u, 0u, 0u, 0u};
+          if constexpr (SL) {
+            R.xu[u][mt][0] = u32x4{0u, 0u, 0u, 0u};
+            R.xu[u][mt][1] = u32x4{0u, 0u, 0u, 0u};
+          }
         }
       }
     }
@@ -258,6 +277,9 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
             xv[mt][0] = u32x4{0u, 0u, 0u, 0u};
             xv[mt][1] = u32x4{0u, 0u, 0u, 0u};
           }
+        } else if constexpr (SL) {
+          xv[mt][0] = sd::silu_mul8<T>(R.x[u][mt][0], R.xu[u][mt][0]);
+          xv[mt][1] = sd::silu_mul8<T>(R.x[u][mt][1], R.xu[u][mt][1]);
         } else {
           xv[mt][0] = R.x[u][mt][0];
           xv[mt][1] = R.x[u][mt][1];
@@ -385,8 +407,11 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
     const int upr = p.K / 8;  // 16-byte units per row
     for (int idx = tid; idx < rows * upr; idx += kThreads) {
       const int r = idx / upr, c = idx - r * upr;
-      sd::store16(xsm + r * p.xpitch + c * 16,
-                  sd::load16(p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8));
+      const uint16_t* src = p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8;
+      if constexpr (SL)
+        sd::store16(xsm + r * p.xpitch + c * 16, sd::silu_mul8<T>(sd::load16(src), sd::load16(src + p.up)));
+      else
+        sd::store16(xsm + r * p.xpitch + c * 16, sd::load16(src));
     }
     // scales (and bias) of the rows every wave of this workgroup owns
     const int per_sub = p.ngmax * RG;
@@ -474,71 +499,114 @@ W8Plan make_plan(int64_t M, int64_t N, int64_t K) {
 }
 
 // Resident workgroups per CU of one kernel instance (cached per device).
-template <typename Kern>
-int resident_wgs(Kern kern) {
-  static int cache[64] = {0};
+// Resident workgroups per CU of kernel `kern` with `smem` bytes of dynamic
+// LDS on the current device, cached per (kernel, device, smem): every
+// instance of the kernel template has the same function type, so the key must
+// be the kernel's address.
+int resident_wgs_of(const void* kern, size_t smem) {
+  struct Entry {
+    const void* kern;
+    int dev;
+    size_t smem;
+    int n;
+  };
+  static Entry table[512];
+  static int used = 0;
+  static std::mutex mu;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i)
+      if (table[i].kern == kern && table[i].dev == dev && table[i].smem == smem) return table[i].n;
+  }
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, 0) != hipSuccess || n <= 0)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, smem) != hipSuccess || n <= 0)
     n = 1;
-  if (dev >= 0 && dev < 64) cache[dev] = n;
+  std::lock_guard<std::mutex> lock(mu);
+  if (used < 512) table[used++] = Entry{kern, dev, smem, n};
   return n;
+}
+
+template <typename Kern>
+int resident_wgs(Kern kern) {
+  return resident_wgs_of(reinterpret_cast<const void*>(kern), 0);
 }
 
 // Activation rows staged in LDS (XL): bytes per row pad and the most a
 // workgroup stages (32 rows of K <= 1024).
 constexpr int kXPad = 16;
 constexpr int kXlMaxBytes = 32 * (1024 * 2 + kXPad);
+// K-split kernels (narrow layers, about one row group per workgroup) stage only
+// when the activation block is large enough to pay for the staging (M > 16
+// rows) and small enough to stage fast (16 rows of K <= 1024), or when the
+// SiLU of a fused down projection is computed there (once per workgroup).
+constexpr int kXlMaxBytesSplit = 16 * (1024 * 2 + kXPad);
 // The most LDS the scale table may take (per group and bias included).
 constexpr int kXlScaleBytes = 32 * 1024;
 
-// Resident workgroups per CU of an XL kernel with `smem` bytes of dynamic LDS
-// (cached per device and activation row count).
 template <typename Kern>
-int resident_wgs_xl(Kern kern, int rows, size_t smem) {
-  static int cache[64][33] = {};
+int resident_wgs_xl(Kern kern, size_t smem) {
+  return resident_wgs_of(reinterpret_cast<const void*>(kern), smem);
+}
+
+// LDS bytes one workgroup may use on the current device (cached per device id).
+int w8_lds_per_block() {
+  static int cache[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  const bool ok = dev >= 0 && dev < 64 && rows >= 1 && rows <= 32;
-  if (ok && cache[dev][rows] > 0) return cache[dev][rows];
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, smem) != hipSuccess || n <= 0)
-    n = 1;
-  if (ok) cache[dev][rows] = n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+      n <= 0)
+    n = 65536;
+  if (dev >= 0 && dev < 64) cache[dev] = n;
   return n;
 }
 
-template <typename T, int MT, int NT, int KW, bool PG>
+// Static LDS of w8a16_kernel<.., MT, NT, KW, U, ..>: the weight tiles and the
+// K-split reduction slot, as the kernel declares them.
+template <int MT, int NT, int KW, int U>
+constexpr size_t w8_static_lds() {
+  return static_cast<size_t>(kWaves) * (16 * NT * 4 * U * 16) +
+         static_cast<size_t>(KW > 1 ? KW - 1 : 1) * (NT * MT * 4) * 64 * 4;
+}
+
+template <typename T, int MT, int NT, int KW, bool PG, bool SL>
 void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
   constexpr int U = NT >= 2 ? 2 : 4;  // 64-k steps per chunk
-  if constexpr (KW == 1) {
+  {
+    // activation rows staged in LDS (XL): wide layers up to kXlMaxBytes (their
+    // occupancy matters); K-split kernels as kXlMaxBytesSplit says
     const int rows = static_cast<int>(p.M < MT * 16 ? p.M : MT * 16);
     const size_t xbytes = static_cast<size_t>(rows) * p.xpitch;
-    if (p.xpitch > 0 && xbytes <= static_cast<size_t>(kXlMaxBytes)) {
+    const size_t xmax = static_cast<size_t>(KW == 1 ? kXlMaxBytes : kXlMaxBytesSplit);
+    if (p.xpitch > 0 && xbytes <= xmax && (KW == 1 || SL || p.M > 16)) {
       // 32 staged rows leave LDS for one workgroup per CU: 8-step chunks (16 KB
       // per wave at NT = 2) keep enough of the weight stream in flight
-      constexpr int UX = MT == 2 ? 8 : U;
-      auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true>;
+      constexpr int UX = MT >= 2 ? 8 : U;
+      constexpr int NSUB = kWaves / KW;
+      auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true, SL>;
       // occupancy from the activation rows; the scale table adds a few KB (per
       // channel: 16 B per row of the workgroup)
-      unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs_xl(kern, rows, xbytes)) /
+      unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs_xl(kern, xbytes)) /
                      grid.y;
       cap = cap >= 8 ? cap / 8 * 8 : 1;
       if (grid.x > cap) grid.x = cap;
       W8Params q = p;
       q.xbytes = static_cast<int32_t>((xbytes + 15) / 16 * 16);
-      q.ngmax = (p.groups + static_cast<int>(grid.x) * kWaves - 1) / (static_cast<int>(grid.x) * kWaves);
+      q.ngmax = (p.groups + static_cast<int>(grid.x) * NSUB - 1) / (static_cast<int>(grid.x) * NSUB);
       const size_t spr = PG ? static_cast<size_t>(p.K / p.group) : 1;
-      const size_t tbl = static_cast<size_t>(kWaves) * q.ngmax * NT * 16 * (spr + (p.bias ? 1 : 0)) * 4;
-      if (tbl <= static_cast<size_t>(kXlScaleBytes)) {
+      const size_t tbl = static_cast<size_t>(NSUB) * q.ngmax * NT * 16 * (spr + (p.bias ? 1 : 0)) * 4;
+      const size_t lds = w8_static_lds<MT, NT, KW, UX>() + q.xbytes + tbl;
+      if (tbl <= static_cast<size_t>(kXlScaleBytes) &&
+          lds <= static_cast<size_t>(w8_lds_per_block())) {
         hipLaunchKernelGGL(kern, grid, dim3(kThreads), q.xbytes + tbl, st, q);
         return;
       }
     }
   }
-  auto kern = w8a16_kernel<T, MT, NT, KW, U, PG>;
+  auto kern = w8a16_kernel<T, MT, NT, KW, U, PG, false, 2, false, SL>;
   // exactly one resident set of workgroups over all activation blocks (a
   // partial second round would leave most of the GPU idle at the end), grid.x
   // a multiple of 8 so that block (x, y) shares an XCD (and its L2) with (x, 0)
@@ -548,29 +616,29 @@ void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, p);
 }
 
-template <typename T, bool PG, int KW>
+template <typename T, bool PG, int KW, bool SL>
 void launch_kw(const W8Params& p, const W8Plan& pl, dim3 grid, hipStream_t st) {
   if constexpr (KW == 1) {
     switch (pl.MT * 8 + pl.NT) {
-      case 1 * 8 + 1: launch_k<T, 1, 1, 1, PG>(p, grid, st); break;
-      case 1 * 8 + 2: launch_k<T, 1, 2, 1, PG>(p, grid, st); break;
-      case 2 * 8 + 1: launch_k<T, 2, 1, 1, PG>(p, grid, st); break;
-      default: launch_k<T, 2, 2, 1, PG>(p, grid, st); break;
+      case 1 * 8 + 1: launch_k<T, 1, 1, 1, PG, SL>(p, grid, st); break;
+      case 1 * 8 + 2: launch_k<T, 1, 2, 1, PG, SL>(p, grid, st); break;
+      case 2 * 8 + 1: launch_k<T, 2, 1, 1, PG, SL>(p, grid, st); break;
+      default: launch_k<T, 2, 2, 1, PG, SL>(p, grid, st); break;
     }
   } else {
-    launch_k<T, 1, 1, KW, PG>(p, grid, st);  // make_plan sets MT = 1 with KW > 1
+    launch_k<T, 1, 1, KW, PG, SL>(p, grid, st);  // make_plan sets MT = 1 with KW > 1
   }
 }
 
-template <typename T>
+template <typename T, bool SL>
 int launch_all(const W8Params& p, const W8Plan& pl, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(pl.grid), static_cast<unsigned>(pl.mblocks));
   if (p.group == 0) {
-    if (pl.KW == 1) launch_kw<T, false, 1>(p, pl, grid, st);
-    else launch_kw<T, false, 4>(p, pl, grid, st);
+    if (pl.KW == 1) launch_kw<T, false, 1, SL>(p, pl, grid, st);
+    else launch_kw<T, false, 4, SL>(p, pl, grid, st);
   } else {
-    if (pl.KW == 1) launch_kw<T, true, 1>(p, pl, grid, st);
-    else launch_kw<T, true, 4>(p, pl, grid, st);
+    if (pl.KW == 1) launch_kw<T, true, 1, SL>(p, pl, grid, st);
+    else launch_kw<T, true, 4, SL>(p, pl, grid, st);
   }
   return sd::check_launch("w8a16");
 }
@@ -585,12 +653,14 @@ extern "C" size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32
   return 0;  // one launch; K splits are reduced inside the workgroup
 }
 
-extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w,
-                               int64_t w_stride_n, const void* scale, int32_t scale_dtype,
-                               int32_t group_size, const void* bias, void* y, int64_t y_stride_m,
-                               int64_t M, int64_t N, int64_t K, int32_t dtype, void* workspace,
-                               size_t workspace_bytes, void* stream) {
-  sd::clear_error();
+namespace {
+
+// Both entry points: up < 0 plain, up >= 0 the activation is SiluAndMul of a
+// gate_up row whose up half starts `up` elements after its gate half.
+int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const int8_t* w, int64_t w_stride_n,
+              const void* scale, int32_t scale_dtype, int32_t group_size, const void* bias,
+              void* y, int64_t y_stride_m, int64_t M, int64_t N, int64_t K, int32_t dtype,
+              void* stream) {
   if (M < 0 || N <= 0 || K <= 0 || group_size < 0) {
     sd::set_error("w8a16: invalid sizes M=%lld N=%lld K=%lld group=%d", (long long)M,
                   (long long)N, (long long)K, group_size);
@@ -622,13 +692,12 @@ extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* 
     sd::set_error("w8a16: dimensions too large");
     return SD_ERR_UNSUPPORTED;
   }
-  if (!sd::aligned16(x) || !sd::aligned16(w) || x_stride_m % 8 != 0 || w_stride_n % 16 != 0) {
-    sd::set_error("w8a16: x and w rows must be 16-byte aligned");
+  if (!sd::aligned16(x) || !sd::aligned16(w) || x_stride_m % 8 != 0 || w_stride_n % 16 != 0 ||
+      (up >= 0 && up % 8 != 0)) {
+    sd::set_error("w8a16: x and w rows (and the up half) must be 16-byte aligned");
     return SD_ERR_UNSUPPORTED;
   }
   const W8Plan pl = make_plan(M, N, K);
-  (void)workspace;
-  (void)workspace_bytes;
   W8Params p;
   p.x = static_cast<const uint16_t*>(x);
   p.xs = x_stride_m;
@@ -647,10 +716,44 @@ extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* 
   p.groups = pl.groups;
   // staged activation rows (wide path): K * 2 bytes + a 16-byte pad per row, so
   // that the 16 rows of a B-operand read start 4 banks apart
-  p.xpitch = K * 2 + kXPad <= 1024 * 2 + kXPad ? static_cast<int32_t>(K * 2 + kXPad) : 0;
+  p.xpitch = K <= 16384 ? static_cast<int32_t>(K * 2 + kXPad) : 0;
   p.xbytes = 0;
   p.ngmax = 0;
+  p.up = up;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == SD_BF16) return launch_all<__bf16>(p, pl, st);
-  return launch_all<_Float16>(p, pl, st);
+  if (up >= 0) {
+    if (dtype == SD_BF16) return launch_all<__bf16, true>(p, pl, st);
+    return launch_all<_Float16, true>(p, pl, st);
+  }
+  if (dtype == SD_BF16) return launch_all<__bf16, false>(p, pl, st);
+  return launch_all<_Float16, false>(p, pl, st);
+}
+
+}  // namespace
+
+extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w,
+                               int64_t w_stride_n, const void* scale, int32_t scale_dtype,
+                               int32_t group_size, const void* bias, void* y, int64_t y_stride_m,
+                               int64_t M, int64_t N, int64_t K, int32_t dtype, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  sd::clear_error();
+  (void)workspace;
+  (void)workspace_bytes;
+  return run_w8a16(x, x_stride_m, -1, w, w_stride_n, scale, scale_dtype, group_size, bias, y,
+                   y_stride_m, M, N, K, dtype, stream);
+}
+
+extern "C" int sd_w8a16_silu_linear(const void* gate_up, int64_t gate_up_stride_m,
+                                    const int8_t* w, int64_t w_stride_n, const void* scale,
+                                    int32_t scale_dtype, int32_t group_size, const void* bias,
+                                    void* y, int64_t y_stride_m, int64_t M, int64_t N, int64_t K,
+                                    int32_t dtype, void* stream) {
+  sd::clear_error();
+  if (gate_up_stride_m < 2 * K) {
+    sd::set_error("w8a16_silu: gate_up rows hold 2 K = %lld elements, stride %lld",
+                  (long long)(2 * K), (long long)gate_up_stride_m);
+    return SD_ERR_VALUE;
+  }
+  return run_w8a16(gate_up, gate_up_stride_m, K, w, w_stride_n, scale, scale_dtype, group_size,
+                   bias, y, y_stride_m, M, N, K, dtype, stream);
 }

@@ -177,7 +177,7 @@ class DraftChain:
                                     slot_mapping=slots)
             h = ops.w8a16_linear(o.reshape(B, Hq * D), *lw["o"])
             x, residual = ops.rmsnorm(h, lw["post_norm"], eps, residual=residual)
-            h = ops.w8a16_linear(ops.silu_mul(ops.w8a16_linear(x, *lw["gate_up"])), *lw["down"])
+            h = ops.w8a16_silu_linear(ops.w8a16_linear(x, *lw["gate_up"]), *lw["down"])
         x, _ = ops.rmsnorm(h, self.final_norm, eps, residual=residual)
         logits = ops.w8a16_linear(x, *self.lm_head)
         ops.sample(logits, out=self.tokens[s + 1])

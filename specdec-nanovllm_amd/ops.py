@@ -262,6 +262,50 @@ def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
     return y.view(*x.shape[:-1], N)
 
 
+
+def w8a16_silu_linear(gate_up: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
+                      bias: torch.Tensor | None = None, group_size: int = 0,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """w8a16_linear(silu_mul(gate_up), ...): the MLP's act_fn and down_proj
+    (layers/activation.py:6-11 then the W8A16 linear). gate_up: (..., 2K); the
+    activation is SiluAndMul's, bit for bit. One launch while the fused form
+    stages its activation rows in LDS (min(M, 16) (2K + 16) <= 33,024 bytes),
+    the two separate launches otherwise (the faster of the two there)."""
+    assert qweight.dtype == torch.int8 and qweight.dim() == 2
+    N, K = qweight.shape
+    g2 = gate_up.reshape(-1, gate_up.shape[-1])
+    M = g2.shape[0]
+    assert g2.shape[1] == 2 * K, f"gate_up {tuple(g2.shape)} needs 2K = {2 * K} columns"
+    if g2.stride(-1) != 1 or (M > 1 and g2.stride(0) % 8 != 0) or g2.data_ptr() % 16:
+        g2 = g2.contiguous()
+    qw = qweight if qweight.is_contiguous() else qweight.contiguous()
+    sc = scale.contiguous()
+    if group_size:
+        assert sc.numel() == N * (K // group_size), "per-group scale must be (N, K // group_size)"
+    else:
+        assert sc.numel() == N, "per-channel scale must have N entries"
+    if min(M, 16) * (2 * K + 16) > 33024:
+        y = w8a16_linear(silu_mul(g2), qw, sc, bias, group_size, out)
+        return y.view(*gate_up.shape[:-1], N)
+    b = None if bias is None else bias.to(gate_up.dtype).contiguous()
+    dev = _lib.require_device(g2, qw, sc, b, out)
+    if out is None:
+        y = torch.empty((M, N), device=dev, dtype=gate_up.dtype)
+    else:
+        y = out.reshape(M, N)
+        assert y.dtype == gate_up.dtype and y.stride(-1) == 1
+    if M == 0:
+        return y.view(*gate_up.shape[:-1], N)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.sd_w8a16_silu_linear(
+            g2.data_ptr(), g2.stride(0), qw.data_ptr(), qw.stride(0),
+            sc.data_ptr(), _lib.dtype_code(sc.dtype), int(group_size), _ptr(b),
+            y.data_ptr(), y.stride(0), M, N, K, _lib.dtype_code(gate_up.dtype),
+            _lib.stream_ptr(dev))
+    _lib.check(rc)
+    return y.view(*gate_up.shape[:-1], N)
+
 def quantize_int8(w: torch.Tensor, group_size: int = 0):
     """Symmetric int8 quantization of a 2-D weight on the GPU (the W8A16
     format's producer, nanovllm/layers/quant.py:123-148): per row (group_size

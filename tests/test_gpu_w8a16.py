@@ -14,7 +14,7 @@ import torch
 
 from conftest import to_np
 from oracle import w8a16 as ow8
-from specdec_nanovllm_amd import ops, workloads
+from specdec_nanovllm_amd import _lib, ops, workloads
 from specdec_nanovllm_amd.layers.linear import ReplicatedLinear
 from specdec_nanovllm_amd.layers.quant import apply_int8_quant, int8_linear, quantize_weight
 
@@ -155,3 +155,30 @@ def test_errors():
         ops.w8a16_linear(c["x"], c["w"].float(), c["s"])
     with pytest.raises(RuntimeError):  # CPU tensors: no fallback
         ops.w8a16_linear(c["x"].cpu(), c["w"].cpu(), c["s"].cpu())
+
+
+@pytest.mark.parametrize("M,N,K,gs,act", [(1, 1024, 3072, 0, torch.bfloat16),
+                                          (7, 1024, 3072, 0, torch.float16),
+                                          (56, 1024, 3072, 0, torch.bfloat16),
+                                          (3, 33000, 1024, 0, torch.bfloat16),
+                                          (20, 33000, 1024, 128, torch.float16)])
+def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
+    # the down projection fed straight from gate_up (narrow K-split path and the
+    # wide path with staged activations): bit-identical to the two-launch form
+    c = workloads.w8a16_case(M, N, K, seed=M + N, act_dtype=act)
+    g = workloads.device_generator(DEV, 17)
+    gu = (torch.randn((M, 2 * K), generator=g, device=DEV) * 2).to(act)
+    s = c["s"] if not gs else (torch.rand((N, K // gs), generator=g, device=DEV) * 3e-3 + 1e-3).to(act)
+    bias = torch.randn((N,), generator=g, device=DEV).to(act)
+    # the C entry point itself (the Python op would take two launches for the
+    # larger activations), then the op
+    lib = _lib.load()
+    fused = torch.empty((M, N), dtype=act, device=DEV)
+    rc = lib.sd_w8a16_silu_linear(gu.data_ptr(), gu.stride(0), c["w"].data_ptr(), c["w"].stride(0),
+                                  s.data_ptr(), _lib.dtype_code(s.dtype), gs, bias.data_ptr(),
+                                  fused.data_ptr(), fused.stride(0), M, N, K, _lib.dtype_code(act),
+                                  _lib.stream_ptr(torch.device(DEV)))
+    _lib.check(rc)
+    two = ops.w8a16_linear(ops.silu_mul(gu), c["w"], s, bias, group_size=gs)
+    assert torch.equal(fused, two)
+    assert torch.equal(ops.w8a16_silu_linear(gu, c["w"], s, bias, group_size=gs), two)
