@@ -274,6 +274,28 @@ int sd_qk_norm_rope(void* q, int64_t q_stride_tok, int64_t q_stride_head, void* 
                     int64_t max_position, int32_t dtype, void* stream);
 
 /*
+ * sd_qk_norm_rope followed by store_kvcache of the finished k rows and of v
+ * (nanovllm/layers/attention.py:33-40), one launch: the draft step's q/k-norm,
+ * RoPE and cache write (models/qwen3.py:80-88 then Attention.forward's store).
+ * No counterpart entry in the reference, which runs them separately. Token t's
+ * k and v rows go to slot slot_mapping[t] of the paged caches
+ * (num_blocks, block_size, num_kv_heads, 128) with the given strides; slot -1
+ * or outside the pool: not written. q, k, the caches: bit for bit what the two
+ * separate calls leave. A token whose position has no cos/sin row stores its
+ * k row unrotated, as it is left in place.
+ */
+int sd_qk_norm_rope_store(void* q, int64_t q_stride_tok, int64_t q_stride_head, void* k,
+                          int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+                          int64_t v_stride_tok, int64_t v_stride_head, int64_t num_tokens,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                          const void* q_weight, const void* k_weight, float eps,
+                          const int64_t* positions, const float* cos_sin,
+                          int64_t cos_sin_stride, int64_t max_position, void* k_cache,
+                          void* v_cache, int64_t cache_stride_block, int64_t cache_stride_pos,
+                          int64_t cache_stride_head, int64_t num_blocks, int32_t block_size,
+                          const int32_t* slot_mapping, int32_t dtype, void* stream);
+
+/*
  * SiluAndMul (nanovllm/layers/activation.py:6-11): x (rows, 2*width) = [gate | up],
  * out (rows, width) = bf16(bf16(silu(gate)) * up). 16-byte aligned rows,
  * width % 8 == 0.

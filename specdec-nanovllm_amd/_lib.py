@@ -72,6 +72,13 @@ SIGNATURES.update({
         _p, _p, _f32,                   # q_weight, k_weight, eps
         _p, _p, _i64, _i64,             # positions, cos_sin, stride, max_position
         _i32, _p]),                     # dtype, stream
+    "sd_qk_norm_rope_store": (ctypes.c_int, [
+        _p, _i64, _i64, _p, _i64, _i64,  # q, strides, k, strides
+        _p, _i64, _i64, _i64,            # v, strides, tokens
+        _i32, _i32, _i32, _p, _p, ctypes.c_float,  # Hq, Hkv, head_dim, q_w, k_w, eps
+        _p, _p, _i64, _i64,              # positions, cos_sin, stride, max_position
+        _p, _p, _i64, _i64, _i64,        # k_cache, v_cache, block/pos/head strides
+        _i64, _i32, _p, _i32, _p]),      # num_blocks, block_size, slots, dtype, stream
     "sd_silu_mul": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i32, _i32, _p]),
     "sd_sample_workspace_size": (ctypes.c_size_t, [_i64, _i32]),
     "sd_sample": (ctypes.c_int, [

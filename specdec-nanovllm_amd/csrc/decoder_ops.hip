@@ -5,7 +5,9 @@
 //   rmsnorm_kernel       RMSNorm.forward, with or without the residual add
 //                        (nanovllm/layers/layernorm.py:16-47)
 //   qk_norm_rope_kernel  per-head q/k RMSNorm then rotate-half RoPE, in place
-//                        (models/qwen3.py:80-88, layers/rotary_embedding.py:6-48)
+//                        (models/qwen3.py:80-88, layers/rotary_embedding.py:6-48),
+//                        optionally with store_kvcache of the finished k rows
+//                        and of v (layers/attention.py:33-40)
 //   silu_mul_kernel      SiluAndMul (layers/activation.py:6-11)
 //   sample_partial_kernel / sample_merge_kernel
 //                        Sampler: temperature + exponential-race (Gumbel-max)
@@ -131,6 +133,15 @@ struct RopeParams {
   const float* cos_sin;  // (max_position, cs_stride): cos[0:64] | sin[64:128]
   int64_t cs_stride;
   int64_t max_pos;
+  // store_kvcache of the finished k rows and of v (kc == NULL: none)
+  const uint16_t* v;
+  int64_t v_stok, v_shead;
+  uint16_t* kc;
+  uint16_t* vc;
+  int64_t c_sblk, c_spos, c_shead;
+  int64_t num_slots;  // num_blocks * block_size
+  int32_t block_size;
+  const int32_t* slot;
 };
 
 template <typename T>
@@ -147,7 +158,29 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(RopeParams p) {
                      : p.k + t * p.k_stok + static_cast<int64_t>(hd - p.Hq) * p.k_shead;
   const uint16_t* w = is_q ? p.qw : p.kw;
   const int64_t pos = p.pos[t];
-  if (pos < 0 || pos >= p.max_pos) return;  // no cos/sin row: the head is left as it is
+  // k heads of a fused store: the row's cache slot (-1 or outside the pool:
+  // not written, as store_kvcache)
+  uint16_t* kdst = nullptr;
+  uint16_t* vdst = nullptr;
+  if (p.kc && !is_q) {
+    const int64_t sl = p.slot[t];
+    if (sl >= 0 && sl < p.num_slots) {
+      const int64_t blk = sl / p.block_size, off = sl - blk * p.block_size;
+      const int64_t row = blk * p.c_sblk + off * p.c_spos + static_cast<int64_t>(hd - p.Hq) * p.c_shead;
+      kdst = p.kc + row;
+      vdst = p.vc + row;
+      const uint16_t* vs = p.v + t * p.v_stok + static_cast<int64_t>(hd - p.Hq) * p.v_shead;
+      vdst[lane] = vs[lane];
+      vdst[lane + 64] = vs[lane + 64];
+    }
+  }
+  if (pos < 0 || pos >= p.max_pos) {  // no cos/sin row: the head is left as it is
+    if (kdst) {
+      kdst[lane] = x[lane];
+      kdst[lane + 64] = x[lane + 64];
+    }
+    return;
+  }
   float x0 = ld<T>(x, lane), x1 = ld<T>(x, lane + 64);
   if (w) {
     float ss = x0 * x0 + x1 * x1;
@@ -161,8 +194,13 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(RopeParams p) {
   const float s = p.cos_sin[pos * p.cs_stride + 64 + lane];
   const float a = x0 * c, b = x1 * s;
   const float e = x1 * c, f = x0 * s;
-  x[lane] = sd::to_bits<T>(a - b);
-  x[lane + 64] = sd::to_bits<T>(e + f);
+  const uint16_t lo = sd::to_bits<T>(a - b), hi = sd::to_bits<T>(e + f);
+  x[lane] = lo;
+  x[lane + 64] = hi;
+  if (kdst) {
+    kdst[lane] = lo;
+    kdst[lane + 64] = hi;
+  }
 }
 
 // ----------------------------------------------------------------- SiLU * up
@@ -358,24 +396,19 @@ extern "C" int sd_rmsnorm(const void* x, int64_t x_stride, const void* residual,
   return sd::check_launch("rmsnorm");
 }
 
-extern "C" int sd_qk_norm_rope(void* q, int64_t q_stride_tok, int64_t q_stride_head, void* k,
-                               int64_t k_stride_tok, int64_t k_stride_head, int64_t num_tokens,
-                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                               const void* q_weight, const void* k_weight, float eps,
-                               const int64_t* positions, const float* cos_sin,
-                               int64_t cos_sin_stride, int64_t max_position, int32_t dtype,
-                               void* stream) {
-  sd::clear_error();
-  if (head_dim != 128 || !is16(dtype) || num_tokens < 0 || num_q_heads < 0 || num_kv_heads < 0 ||
-      max_position <= 0 || cos_sin_stride < 128) {
+namespace {
+
+int run_qk_norm_rope(RopeParams p, int32_t head_dim, int32_t dtype, void* stream) {
+  if (head_dim != 128 || !is16(dtype) || p.tokens < 0 || p.Hq < 0 || p.Hkv < 0 ||
+      p.max_pos <= 0 || p.cs_stride < 128) {
     sd::set_error("qk_norm_rope: head_dim 128 and bf16/fp16 only, cos_sin rows of >= 128 "
                   "floats (head_dim=%d dtype=%d stride=%lld)", head_dim, dtype,
-                  (long long)cos_sin_stride);
+                  (long long)p.cs_stride);
     return SD_ERR_UNSUPPORTED;
   }
-  const int64_t items = num_tokens * (num_q_heads + num_kv_heads);
+  const int64_t items = p.tokens * (p.Hq + p.Hkv);
   if (items == 0) return SD_OK;
-  if ((num_q_heads && !q) || (num_kv_heads && !k) || !positions || !cos_sin) {
+  if ((p.Hq && !p.q) || (p.Hkv && !p.k) || !p.pos || !p.cos_sin) {
     sd::set_error("qk_norm_rope: null pointer argument");
     return SD_ERR_VALUE;
   }
@@ -384,16 +417,91 @@ extern "C" int sd_qk_norm_rope(void* q, int64_t q_stride_tok, int64_t q_stride_h
     sd::set_error("qk_norm_rope: too many heads (%lld)", (long long)items);
     return SD_ERR_UNSUPPORTED;
   }
-  RopeParams p{static_cast<uint16_t*>(q), q_stride_tok, q_stride_head, static_cast<uint16_t*>(k),
-               k_stride_tok, k_stride_head, num_tokens, num_q_heads, num_kv_heads,
-               static_cast<const uint16_t*>(q_weight), static_cast<const uint16_t*>(k_weight), eps,
-               positions, cos_sin, cos_sin_stride, max_position};
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == SD_BF16)
     hipLaunchKernelGGL(qk_norm_rope_kernel<__bf16>, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0, st, p);
   else
     hipLaunchKernelGGL(qk_norm_rope_kernel<_Float16>, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0, st, p);
   return sd::check_launch("qk_norm_rope");
+}
+
+}  // namespace
+
+extern "C" int sd_qk_norm_rope(void* q, int64_t q_stride_tok, int64_t q_stride_head, void* k,
+                               int64_t k_stride_tok, int64_t k_stride_head, int64_t num_tokens,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               const void* q_weight, const void* k_weight, float eps,
+                               const int64_t* positions, const float* cos_sin,
+                               int64_t cos_sin_stride, int64_t max_position, int32_t dtype,
+                               void* stream) {
+  sd::clear_error();
+  RopeParams p{};
+  p.q = static_cast<uint16_t*>(q);
+  p.q_stok = q_stride_tok;
+  p.q_shead = q_stride_head;
+  p.k = static_cast<uint16_t*>(k);
+  p.k_stok = k_stride_tok;
+  p.k_shead = k_stride_head;
+  p.tokens = num_tokens;
+  p.Hq = num_q_heads;
+  p.Hkv = num_kv_heads;
+  p.qw = static_cast<const uint16_t*>(q_weight);
+  p.kw = static_cast<const uint16_t*>(k_weight);
+  p.eps = eps;
+  p.pos = positions;
+  p.cos_sin = cos_sin;
+  p.cs_stride = cos_sin_stride;
+  p.max_pos = max_position;
+  return run_qk_norm_rope(p, head_dim, dtype, stream);
+}
+
+extern "C" int sd_qk_norm_rope_store(void* q, int64_t q_stride_tok, int64_t q_stride_head, void* k,
+                                     int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+                                     int64_t v_stride_tok, int64_t v_stride_head,
+                                     int64_t num_tokens, int32_t num_q_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, const void* q_weight,
+                                     const void* k_weight, float eps, const int64_t* positions,
+                                     const float* cos_sin, int64_t cos_sin_stride,
+                                     int64_t max_position, void* k_cache, void* v_cache,
+                                     int64_t cache_stride_block, int64_t cache_stride_pos,
+                                     int64_t cache_stride_head, int64_t num_blocks,
+                                     int32_t block_size, const int32_t* slot_mapping,
+                                     int32_t dtype, void* stream) {
+  sd::clear_error();
+  if (num_tokens > 0 && num_kv_heads > 0 &&
+      (!v || !k_cache || !v_cache || !slot_mapping || block_size <= 0 || num_blocks <= 0)) {
+    sd::set_error("qk_norm_rope_store: v, caches, slot_mapping and a positive pool needed");
+    return SD_ERR_VALUE;
+  }
+  RopeParams p{};
+  p.q = static_cast<uint16_t*>(q);
+  p.q_stok = q_stride_tok;
+  p.q_shead = q_stride_head;
+  p.k = static_cast<uint16_t*>(k);
+  p.k_stok = k_stride_tok;
+  p.k_shead = k_stride_head;
+  p.tokens = num_tokens;
+  p.Hq = num_q_heads;
+  p.Hkv = num_kv_heads;
+  p.qw = static_cast<const uint16_t*>(q_weight);
+  p.kw = static_cast<const uint16_t*>(k_weight);
+  p.eps = eps;
+  p.pos = positions;
+  p.cos_sin = cos_sin;
+  p.cs_stride = cos_sin_stride;
+  p.max_pos = max_position;
+  p.v = static_cast<const uint16_t*>(v);
+  p.v_stok = v_stride_tok;
+  p.v_shead = v_stride_head;
+  p.kc = static_cast<uint16_t*>(k_cache);
+  p.vc = static_cast<uint16_t*>(v_cache);
+  p.c_sblk = cache_stride_block;
+  p.c_spos = cache_stride_pos;
+  p.c_shead = cache_stride_head;
+  p.num_slots = num_blocks * block_size;
+  p.block_size = block_size;
+  p.slot = slot_mapping;
+  return run_qk_norm_rope(p, head_dim, dtype, stream);
 }
 
 extern "C" int sd_silu_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride,

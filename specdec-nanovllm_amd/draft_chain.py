@@ -171,10 +171,11 @@ class DraftChain:
             q = qkv[:, :Hq * D].view(B, Hq, D)
             kk = qkv[:, Hq * D:(Hq + Hkv) * D].view(B, Hkv, D)
             v = qkv[:, (Hq + Hkv) * D:].view(B, Hkv, D)
-            ops.qk_norm_rope(q, kk, pos, self.cos_sin, lw["q_norm"], lw["k_norm"], eps)
+            # q/k-norm + RoPE + store_kvcache in one launch, then plain paged attention
+            ops.qk_norm_rope(q, kk, pos, self.cos_sin, lw["q_norm"], lw["k_norm"], eps, v=v,
+                             k_cache=self.kv[0, li], v_cache=self.kv[1, li], slot_mapping=slots)
             o = ops.paged_attention(q, self.kv[0, li], self.kv[1, li], self.block_table,
-                                    self.scale, context_lens=ctx, key=kk, value=v,
-                                    slot_mapping=slots)
+                                    self.scale, context_lens=ctx)
             h = ops.w8a16_linear(o.reshape(B, Hq * D), *lw["o"])
             x, residual = ops.rmsnorm(h, lw["post_norm"], eps, residual=residual)
             h = ops.w8a16_silu_linear(ops.w8a16_linear(x, *lw["gate_up"]), *lw["down"])

@@ -375,12 +375,19 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
 
 def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor,
                  cos_sin_cache: torch.Tensor, q_weight: torch.Tensor | None = None,
-                 k_weight: torch.Tensor | None = None, eps: float = 1e-6) -> None:
+                 k_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                 v: torch.Tensor | None = None, k_cache: torch.Tensor | None = None,
+                 v_cache: torch.Tensor | None = None,
+                 slot_mapping: torch.Tensor | None = None) -> None:
     """In place on q (T, Hq, 128) and k (T, Hkv, 128) (strided views allowed):
     per-head RMSNorm with q_weight / k_weight (skipped when None), then
     rotate-half RoPE at ``positions`` from ``cos_sin_cache`` (max_pos, [1,] 128)
     fp32 = [cos | sin] (nanovllm/models/qwen3.py:80-88,
-    layers/rotary_embedding.py:6-48)."""
+    layers/rotary_embedding.py:6-48).
+
+    With ``v``, ``k_cache``, ``v_cache`` and ``slot_mapping``: also
+    store_kvcache of the finished k rows and of v (layers/attention.py:33-40)
+    in the same launch; caches (num_blocks, block_size, Hkv, 128)."""
     assert q.dim() == 3 and k.dim() == 3 and q.shape[0] == k.shape[0]
     assert q.shape[-1] == 128 and k.shape[-1] == 128 and q.stride(-1) == 1 and k.stride(-1) == 1
     assert q.dtype == k.dtype
@@ -399,6 +406,24 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor,
     if T == 0:
         return
     lib = _lib.load()
+    if k_cache is not None:
+        assert v is not None and v_cache is not None and slot_mapping is not None
+        assert v.shape == k.shape and v.stride(-1) == 1 and v.dtype == k.dtype
+        assert k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride()
+        assert k_cache.dtype == k.dtype and k_cache.shape[2:] == k.shape[1:]
+        slots = _i32(slot_mapping.reshape(-1)).contiguous()
+        assert slots.numel() == T
+        _lib.require_device(v, k_cache, v_cache, slots)
+        with torch.cuda.device(dev):
+            rc = lib.sd_qk_norm_rope_store(
+                q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+                v.data_ptr(), v.stride(0), v.stride(1), T, q.shape[1], k.shape[1], 128,
+                _ptr(qw), _ptr(kw), float(eps), pos.data_ptr(), cs.data_ptr(), cs.stride(0),
+                cs.shape[0], k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+                k_cache.stride(1), k_cache.stride(2), k_cache.shape[0], k_cache.shape[1],
+                slots.data_ptr(), _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
+        _lib.check(rc)
+        return
     with torch.cuda.device(dev):
         rc = lib.sd_qk_norm_rope(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
                                  k.stride(1), T, q.shape[1], k.shape[1], 128, _ptr(qw), _ptr(kw),

@@ -123,6 +123,33 @@ def test_rope_position_zero_and_out_of_range():
     assert torch.equal(q, q0) and torch.equal(k, k0)
 
 
+@pytest.mark.parametrize("dt,bs", [("bf16", 256), ("f16", 16)])
+def test_qk_norm_rope_store_is_rope_then_store(dt, bs):
+    # one launch = qk_norm_rope then store_kvcache: q, k and both caches bit for bit;
+    # slot -1 rows are not written, a position without a cos/sin row stores k as is
+    D, T, hq, hkv, nblk = 128, 6, 16, 8, 5
+    qkv = rand((T, (hq + 2 * hkv) * D), 40 + bs, DT[dt]).to(DEV)
+    q = qkv[:, :hq * D].view(T, hq, D)
+    k = qkv[:, hq * D:(hq + hkv) * D].view(T, hkv, D)
+    v = qkv[:, (hq + hkv) * D:].view(T, hkv, D)
+    qw, kw = rand((D,), 3, DT[dt]).to(DEV), rand((D,), 4, DT[dt]).to(DEV)
+    cs = torch.from_numpy(od.rope_cache(512, D, 1e6)).to(DEV)
+    pos = torch.tensor([5, 0, 511, 512, 100, 7], device=DEV)
+    slots = torch.tensor([3, -1, nblk * bs - 1, 9, 2 * bs, nblk * bs], dtype=torch.int32, device=DEV)
+    kc = rand((nblk, bs, hkv, D), 5, DT[dt]).to(DEV)
+    vc = rand((nblk, bs, hkv, D), 6, DT[dt]).to(DEV)
+    qkv2, kc2, vc2 = qkv.clone(), kc.clone(), vc.clone()
+    q2 = qkv2[:, :hq * D].view(T, hq, D)
+    k2 = qkv2[:, hq * D:(hq + hkv) * D].view(T, hkv, D)
+    v2 = qkv2[:, (hq + hkv) * D:].view(T, hkv, D)
+    ops.qk_norm_rope(q, k, pos, cs, qw, kw, 1e-6, v=v, k_cache=kc, v_cache=vc, slot_mapping=slots)
+    ops.qk_norm_rope(q2, k2, pos, cs, qw, kw, 1e-6)
+    ops.store_kvcache(k2, v2, kc2, vc2, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(qkv, qkv2)
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+
+
 # ------------------------------------------------------------------ SiLU*up
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("rows,I", [(1, 3072), (16, 3072), (56, 9728), (3, 8)])
