@@ -221,6 +221,34 @@ int sd_w8a16_silu_linear(const void* gate_up, int64_t gate_up_stride_m, const in
                          int64_t M, int64_t N, int64_t K, int32_t dtype, void* stream);
 
 /*
+ * add + RMSNorm fused into the W8A16 linear: y = norm(x [+ residual]) @
+ * (w * scale)^T (+ bias), with norm the sd_rmsnorm row above (the decoder
+ * layer's input_layernorm / post_attention_layernorm followed by qkv_proj /
+ * gate_up_proj, models/qwen3.py Qwen3DecoderLayer.forward). No counterpart
+ * entry in the reference: the fusion saves the RMSNorm launch and its round
+ * trip through memory. The normalised row equals sd_rmsnorm's out bit for bit,
+ * so y equals sd_rmsnorm followed by sd_w8a16_linear; with a residual,
+ * residual_out (may be NULL) receives bf16(x + residual) as sd_rmsnorm's
+ * residual_out does, written by one workgroup per row block. residual_out may
+ * alias neither x nor residual (other workgroups still read them). Each
+ * workgroup normalises its activation rows, one after another, while staging
+ * them in LDS: the form pays for a few rows (decode: about 1.4 us saved at
+ * M = 1 on MI355X, break-even near M = 5), not for many. A block that does not
+ * fit (min(M, 16) (2 K + 16) > 33,024 bytes is never promised) returns
+ * SD_ERR_UNSUPPORTED and the caller runs the two calls.
+ *   x, residual, residual_out: (M, K) dtype, 16-byte aligned rows;
+ *   norm_weight: (K,) dtype; K % 8 == 0, K <= 8192; the rest as
+ *   sd_w8a16_linear (no workspace).
+ */
+int sd_w8a16_rmsnorm_linear(const void* x, int64_t x_stride_m, const void* residual,
+                            int64_t residual_stride_m, void* residual_out,
+                            int64_t residual_out_stride_m, const void* norm_weight, float eps,
+                            const int8_t* w, int64_t w_stride_n, const void* scale,
+                            int32_t scale_dtype, int32_t group_size, const void* bias, void* y,
+                            int64_t y_stride_m, int64_t M, int64_t N, int64_t K, int32_t dtype,
+                            void* stream);
+
+/*
  * Symmetric int8 weight quantization, the producer of the W8A16 format:
  * `quantize_weight` (nanovllm/layers/quant.py:123-148) and the offline
  * converter's `quantize_tensor` (scripts/quantize_int8.py:53-83). Per row and

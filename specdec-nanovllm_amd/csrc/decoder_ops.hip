@@ -69,51 +69,11 @@ struct NormParams {
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(NormParams p) {
-#pragma clang fp contract(off)
   __shared__ float red[kThreads / 64];
   const int64_t row = blockIdx.x;
-  const uint16_t* x = p.x + row * p.xs;
-  float v[kChunks][8];
-  float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    const int e0 = (c * kThreads + threadIdx.x) * 8;
-    if (e0 < p.H) {
-      const sd::u32x4 a = sd::load16(x + e0);
-      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
-      sd::u32x4 b = {0u, 0u, 0u, 0u};
-      if (p.res) b = sd::load16(p.res + row * p.rs + e0);
-      const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float f = sd::from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
-        if (p.res) f = f + sd::from_bits<T>(static_cast<uint16_t>(bw[i / 2] >> (16 * (i & 1))));
-        v[c][i] = f;
-        ss += f * f;
-      }
-    }
-  }
-  const float var = block_sum(ss, red) / static_cast<float>(p.H);
-  const float r = rsqrtf(var + p.eps);
-#pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    const int e0 = (c * kThreads + threadIdx.x) * 8;
-    if (e0 < p.H) {
-      const sd::u32x4 wv = sd::load16(p.w + e0);
-      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
-      uint32_t o[4], ro[4];
-#pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        const float w0 = sd::from_bits<T>(static_cast<uint16_t>(ww[i / 2]));
-        const float w1 = sd::from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> 16));
-        o[i / 2] = sd::pack2<T>(round16<T>(v[c][i] * r) * w0, round16<T>(v[c][i + 1] * r) * w1);
-        ro[i / 2] = sd::pack2<T>(v[c][i], v[c][i + 1]);
-      }
-      sd::store16(p.out + row * p.os + e0, sd::u32x4{o[0], o[1], o[2], o[3]});
-      if (p.res && p.res_out)
-        sd::store16(p.res_out + row * p.ros + e0, sd::u32x4{ro[0], ro[1], ro[2], ro[3]});
-    }
-  }
+  sd::add_rmsnorm_row<T>(p.x + row * p.xs, p.res ? p.res + row * p.rs : nullptr, p.w, p.H, p.eps,
+                         red, p.out + row * p.os,
+                         p.res && p.res_out ? p.res_out + row * p.ros : nullptr);
 }
 
 // ----------------------------------------------------------- q/k norm + RoPE

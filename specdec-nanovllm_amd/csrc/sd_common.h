@@ -109,6 +109,72 @@ __device__ __forceinline__ float sum_over_groups(float v) {
 // results below 2^-126 flush to 0, 2^-inf = 0. Softmax weights only.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Add + RMSNorm of one row by the 256 threads of a workgroup (every thread
+// calls it; it synchronises the workgroup): h = x (+ res) in fp32,
+// out = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * w), res_out = bf16(h) (when
+// res_out). Thread t holds the 8-element chunks t, t + 256, ... (H <= 8192,
+// H % 8 == 0); the sum of squares runs per thread over its chunks, then over
+// the wave (xor shuffles 32 .. 1), then over the 4 waves in order, so any two
+// callers produce the same bits. `red` holds 4 floats of LDS; `out` may be a
+// global or an LDS row.
+template <typename T>
+__device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_t* res,
+                                                const uint16_t* w, int H, float eps, float* red,
+                                                uint16_t* out, uint16_t* res_out) {
+#pragma clang fp contract(off)
+  constexpr int kChunks = 4;
+  float v[kChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e0 = (c * 256 + static_cast<int>(threadIdx.x)) * 8;
+    if (e0 < H) {
+      const u32x4 a = load16(x + e0);
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+      u32x4 b = {0u, 0u, 0u, 0u};
+      if (res) b = load16(res + e0);
+      const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float f = from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
+        if (res) f = f + from_bits<T>(static_cast<uint16_t>(bw[i / 2] >> (16 * (i & 1))));
+        v[c][i] = f;
+        ss += f * f;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int wv = 0; wv < 4; ++wv) tot += red[wv];
+  __syncthreads();  // red is free for the next row
+  const float r = rsqrtf(tot / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e0 = (c * 256 + static_cast<int>(threadIdx.x)) * 8;
+    if (e0 < H) {
+      const u32x4 wv = load16(w + e0);
+      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t o[4], ro[4];
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const float w0 = from_bits<T>(static_cast<uint16_t>(ww[i / 2]));
+        const float w1 = from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> 16));
+        const float n0 = static_cast<float>(static_cast<T>(v[c][i] * r));
+        const float n1 = static_cast<float>(static_cast<T>(v[c][i + 1] * r));
+        o[i / 2] = pack2<T>(n0 * w0, n1 * w1);
+        ro[i / 2] = pack2<T>(v[c][i], v[c][i + 1]);
+      }
+      store16(out + e0, u32x4{o[0], o[1], o[2], o[3]});
+      if (res_out) store16(res_out + e0, u32x4{ro[0], ro[1], ro[2], ro[3]});
+    }
+  }
+}
+
 // SiluAndMul on 8 elements: bf16(bf16(silu(g)) * u) per element (T = the
 // activation type), the eager module's roundings; g and u are 8 packed 16-bit
 // values each. Shared by the SiLU kernel and the W8A16 activation path that

@@ -56,6 +56,13 @@ struct W8Params {
   int32_t xbytes;  // XL: bytes of staged activation rows; the scale table follows
   int32_t ngmax;   // XL: most row groups one wave owns
   int64_t up;      // SL: elements from a gate_up row's gate half to its up half
+  // NM: add + RMSNorm of the activation rows while staging them
+  const uint16_t* nw;   // (K,) norm weight
+  const uint16_t* nres; // (M, K) residual added first, or NULL
+  int64_t nres_s;
+  uint16_t* nres_out;   // (M, K) bf16(x + residual), written by workgroup x = 0, or NULL
+  int64_t nres_out_s;
+  float neps;
 };
 
 __device__ __forceinline__ float load_scale(const void* s, int dtype, int64_t i) {
@@ -122,12 +129,19 @@ template <> __device__ __forceinline__ u32x4 dequant8<__bf16>(uint32_t w0, uint3
 // lanes active), and every vector load instruction costs the compute unit's
 // address path the same time whatever its lane count.
 //
-// SL: the activation is SiluAndMul of a gate_up row, bf16(bf16(silu(g)) * u)
-// with g = x[m, k] and u = x[m, up + k], formed where the activation is loaded
-// (the down projection reads the gate_up projection's output directly).
+// MODE 1 (SL): the activation is SiluAndMul of a gate_up row,
+// bf16(bf16(silu(g)) * u) with g = x[m, k] and u = x[m, up + k], formed where
+// the activation is loaded (the down projection reads the gate_up projection's
+// output directly).
+// MODE 2 (NM, staged only): the activation is the add + RMSNorm of the rows
+// (sd::add_rmsnorm_row, the RMSNorm kernel's own arithmetic), formed while
+// staging; workgroup x = 0 of each activation block writes the new residual.
 template <typename T, int MT, int NT, int KW, int U, bool PER_GROUP, bool CONTIG = false,
-          int D = 2, bool XL = false, bool SL = false>
+          int D = 2, bool XL = false, int MODE = 0>
 __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
+  constexpr bool SL = MODE == 1;
+  constexpr bool NM = MODE == 2;
+  static_assert(!NM || XL, "the norm is formed while staging");
   static_assert(U == 2 || U == 4 || U == 8, "a chunk row segment is 64 U bytes");
   constexpr int LPR = 4 * U;         // lanes per row segment (16-byte units per row)
   constexpr int RPI = 64 / LPR;      // row segments per load instruction
@@ -405,13 +419,27 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
     // prefetch, so their latencies overlap; every wave of the workgroup takes part
     const int rows = min(MT * 16, p.M - m0);
     const int upr = p.K / 8;  // 16-byte units per row
-    for (int idx = tid; idx < rows * upr; idx += kThreads) {
-      const int r = idx / upr, c = idx - r * upr;
-      const uint16_t* src = p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8;
-      if constexpr (SL)
-        sd::store16(xsm + r * p.xpitch + c * 16, sd::silu_mul8<T>(sd::load16(src), sd::load16(src + p.up)));
-      else
-        sd::store16(xsm + r * p.xpitch + c * 16, sd::load16(src));
+    if constexpr (NM) {
+      // rows one after another, each by the whole workgroup (the registers hold
+      // it between the two passes); one workgroup per row block writes the
+      // residual sum. Every workgroup repeats this for its block: it pays for
+      // a few rows (decode), not for many.
+      uint16_t* ro = p.nres && p.nres_out && blockIdx.x == 0 ? p.nres_out + m0 * p.nres_out_s : nullptr;
+      const uint16_t* res = p.nres ? p.nres + m0 * p.nres_s : nullptr;
+      __shared__ float nred[kThreads / 64];
+      for (int r = 0; r < rows; ++r)
+        sd::add_rmsnorm_row<T>(p.x + (m0 + r) * p.xs, res ? res + r * p.nres_s : nullptr, p.nw, p.K,
+                               p.neps, nred, reinterpret_cast<uint16_t*>(xsm + r * p.xpitch),
+                               ro ? ro + r * p.nres_out_s : nullptr);
+    } else {
+      for (int idx = tid; idx < rows * upr; idx += kThreads) {
+        const int r = idx / upr, c = idx - r * upr;
+        const uint16_t* src = p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8;
+        if constexpr (SL)
+          sd::store16(xsm + r * p.xpitch + c * 16, sd::silu_mul8<T>(sd::load16(src), sd::load16(src + p.up)));
+        else
+          sd::store16(xsm + r * p.xpitch + c * 16, sd::load16(src));
+      }
     }
     // scales (and bias) of the rows every wave of this workgroup owns
     const int per_sub = p.ngmax * RG;
@@ -572,8 +600,8 @@ constexpr size_t w8_static_lds() {
          static_cast<size_t>(KW > 1 ? KW - 1 : 1) * (NT * MT * 4) * 64 * 4;
 }
 
-template <typename T, int MT, int NT, int KW, bool PG, bool SL>
-void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
+template <typename T, int MT, int NT, int KW, bool PG, int MODE>
+int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
   constexpr int U = NT >= 2 ? 2 : 4;  // 64-k steps per chunk
   {
     // activation rows staged in LDS (XL): wide layers up to kXlMaxBytes (their
@@ -581,12 +609,12 @@ void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
     const int rows = static_cast<int>(p.M < MT * 16 ? p.M : MT * 16);
     const size_t xbytes = static_cast<size_t>(rows) * p.xpitch;
     const size_t xmax = static_cast<size_t>(KW == 1 ? kXlMaxBytes : kXlMaxBytesSplit);
-    if (p.xpitch > 0 && xbytes <= xmax && (KW == 1 || SL || p.M > 16)) {
+    if (p.xpitch > 0 && xbytes <= xmax && (KW == 1 || MODE != 0 || p.M > 16)) {
       // 32 staged rows leave LDS for one workgroup per CU: 8-step chunks (16 KB
       // per wave at NT = 2) keep enough of the weight stream in flight
       constexpr int UX = MT >= 2 ? 8 : U;
       constexpr int NSUB = kWaves / KW;
-      auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true, SL>;
+      auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true, MODE>;
       // occupancy from the activation rows; the scale table adds a few KB (per
       // channel: 16 B per row of the workgroup)
       unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs_xl(kern, xbytes)) /
@@ -602,44 +630,54 @@ void launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
       if (tbl <= static_cast<size_t>(kXlScaleBytes) &&
           lds <= static_cast<size_t>(w8_lds_per_block())) {
         hipLaunchKernelGGL(kern, grid, dim3(kThreads), q.xbytes + tbl, st, q);
-        return;
+        return SD_OK;
       }
     }
   }
-  auto kern = w8a16_kernel<T, MT, NT, KW, U, PG, false, 2, false, SL>;
-  // exactly one resident set of workgroups over all activation blocks (a
-  // partial second round would leave most of the GPU idle at the end), grid.x
-  // a multiple of 8 so that block (x, y) shares an XCD (and its L2) with (x, 0)
-  unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs(kern)) / grid.y;
-  cap = cap >= 8 ? cap / 8 * 8 : 1;
-  if (grid.x > cap) grid.x = cap;
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, p);
+  if constexpr (MODE == 2) {
+    // the norm needs the rows staged: no register form
+    sd::set_error("w8a16_rmsnorm: the activation block (%d rows of K = %d) does not fit the "
+                  "staging LDS", static_cast<int>(p.M < MT * 16 ? p.M : MT * 16), p.K);
+    return SD_ERR_UNSUPPORTED;
+  } else {
+    auto kern = w8a16_kernel<T, MT, NT, KW, U, PG, false, 2, false, MODE>;
+    // exactly one resident set of workgroups over all activation blocks (a
+    // partial second round would leave most of the GPU idle at the end), grid.x
+    // a multiple of 8 so that block (x, y) shares an XCD (and its L2) with (x, 0)
+    unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs(kern)) / grid.y;
+    cap = cap >= 8 ? cap / 8 * 8 : 1;
+    if (grid.x > cap) grid.x = cap;
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, p);
+    return SD_OK;
+  }
 }
 
-template <typename T, bool PG, int KW, bool SL>
-void launch_kw(const W8Params& p, const W8Plan& pl, dim3 grid, hipStream_t st) {
+template <typename T, bool PG, int KW, int MODE>
+int launch_kw(const W8Params& p, const W8Plan& pl, dim3 grid, hipStream_t st) {
   if constexpr (KW == 1) {
     switch (pl.MT * 8 + pl.NT) {
-      case 1 * 8 + 1: launch_k<T, 1, 1, 1, PG, SL>(p, grid, st); break;
-      case 1 * 8 + 2: launch_k<T, 1, 2, 1, PG, SL>(p, grid, st); break;
-      case 2 * 8 + 1: launch_k<T, 2, 1, 1, PG, SL>(p, grid, st); break;
-      default: launch_k<T, 2, 2, 1, PG, SL>(p, grid, st); break;
+      case 1 * 8 + 1: return launch_k<T, 1, 1, 1, PG, MODE>(p, grid, st);
+      case 1 * 8 + 2: return launch_k<T, 1, 2, 1, PG, MODE>(p, grid, st);
+      case 2 * 8 + 1: return launch_k<T, 2, 1, 1, PG, MODE>(p, grid, st);
+      default: return launch_k<T, 2, 2, 1, PG, MODE>(p, grid, st);
     }
   } else {
-    launch_k<T, 1, 1, KW, PG, SL>(p, grid, st);  // make_plan sets MT = 1 with KW > 1
+    return launch_k<T, 1, 1, KW, PG, MODE>(p, grid, st);  // make_plan sets MT = 1 with KW > 1
   }
 }
 
-template <typename T, bool SL>
+template <typename T, int MODE>
 int launch_all(const W8Params& p, const W8Plan& pl, hipStream_t st) {
+  int rc;
   const dim3 grid(static_cast<unsigned>(pl.grid), static_cast<unsigned>(pl.mblocks));
   if (p.group == 0) {
-    if (pl.KW == 1) launch_kw<T, false, 1, SL>(p, pl, grid, st);
-    else launch_kw<T, false, 4, SL>(p, pl, grid, st);
+    if (pl.KW == 1) rc = launch_kw<T, false, 1, MODE>(p, pl, grid, st);
+    else rc = launch_kw<T, false, 4, MODE>(p, pl, grid, st);
   } else {
-    if (pl.KW == 1) launch_kw<T, true, 1, SL>(p, pl, grid, st);
-    else launch_kw<T, true, 4, SL>(p, pl, grid, st);
+    if (pl.KW == 1) rc = launch_kw<T, true, 1, MODE>(p, pl, grid, st);
+    else rc = launch_kw<T, true, 4, MODE>(p, pl, grid, st);
   }
+  if (rc != SD_OK) return rc;
   return sd::check_launch("w8a16");
 }
 
@@ -655,12 +693,22 @@ extern "C" size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32
 
 namespace {
 
-// Both entry points: up < 0 plain, up >= 0 the activation is SiluAndMul of a
-// gate_up row whose up half starts `up` elements after its gate half.
-int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const int8_t* w, int64_t w_stride_n,
-              const void* scale, int32_t scale_dtype, int32_t group_size, const void* bias,
-              void* y, int64_t y_stride_m, int64_t M, int64_t N, int64_t K, int32_t dtype,
-              void* stream) {
+// Activation forms of the entry points: plain; SiluAndMul of a gate_up row
+// whose up half starts `up` elements after its gate half (up >= 0); add +
+// RMSNorm (norm->weight != NULL).
+struct NormArgs {
+  const void* weight;  // NULL: no norm
+  const void* residual;
+  int64_t residual_stride;
+  void* residual_out;
+  int64_t residual_out_stride;
+  float eps;
+};
+
+int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& norm,
+              const int8_t* w, int64_t w_stride_n, const void* scale, int32_t scale_dtype,
+              int32_t group_size, const void* bias, void* y, int64_t y_stride_m, int64_t M,
+              int64_t N, int64_t K, int32_t dtype, void* stream) {
   if (M < 0 || N <= 0 || K <= 0 || group_size < 0) {
     sd::set_error("w8a16: invalid sizes M=%lld N=%lld K=%lld group=%d", (long long)M,
                   (long long)N, (long long)K, group_size);
@@ -720,13 +768,23 @@ int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const int8_t* w, in
   p.xbytes = 0;
   p.ngmax = 0;
   p.up = up;
+  p.nw = static_cast<const uint16_t*>(norm.weight);
+  p.nres = static_cast<const uint16_t*>(norm.residual);
+  p.nres_s = norm.residual_stride;
+  p.nres_out = static_cast<uint16_t*>(norm.residual_out);
+  p.nres_out_s = norm.residual_out_stride;
+  p.neps = norm.eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (up >= 0) {
-    if (dtype == SD_BF16) return launch_all<__bf16, true>(p, pl, st);
-    return launch_all<_Float16, true>(p, pl, st);
+    if (dtype == SD_BF16) return launch_all<__bf16, 1>(p, pl, st);
+    return launch_all<_Float16, 1>(p, pl, st);
   }
-  if (dtype == SD_BF16) return launch_all<__bf16, false>(p, pl, st);
-  return launch_all<_Float16, false>(p, pl, st);
+  if (p.nw) {
+    if (dtype == SD_BF16) return launch_all<__bf16, 2>(p, pl, st);
+    return launch_all<_Float16, 2>(p, pl, st);
+  }
+  if (dtype == SD_BF16) return launch_all<__bf16, 0>(p, pl, st);
+  return launch_all<_Float16, 0>(p, pl, st);
 }
 
 }  // namespace
@@ -739,8 +797,8 @@ extern "C" int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* 
   sd::clear_error();
   (void)workspace;
   (void)workspace_bytes;
-  return run_w8a16(x, x_stride_m, -1, w, w_stride_n, scale, scale_dtype, group_size, bias, y,
-                   y_stride_m, M, N, K, dtype, stream);
+  return run_w8a16(x, x_stride_m, -1, NormArgs{}, w, w_stride_n, scale, scale_dtype, group_size,
+                   bias, y, y_stride_m, M, N, K, dtype, stream);
 }
 
 extern "C" int sd_w8a16_silu_linear(const void* gate_up, int64_t gate_up_stride_m,
@@ -754,6 +812,36 @@ extern "C" int sd_w8a16_silu_linear(const void* gate_up, int64_t gate_up_stride_
                   (long long)(2 * K), (long long)gate_up_stride_m);
     return SD_ERR_VALUE;
   }
-  return run_w8a16(gate_up, gate_up_stride_m, K, w, w_stride_n, scale, scale_dtype, group_size,
-                   bias, y, y_stride_m, M, N, K, dtype, stream);
+  return run_w8a16(gate_up, gate_up_stride_m, K, NormArgs{}, w, w_stride_n, scale, scale_dtype,
+                   group_size, bias, y, y_stride_m, M, N, K, dtype, stream);
+}
+
+extern "C" int sd_w8a16_rmsnorm_linear(const void* x, int64_t x_stride_m, const void* residual,
+                                       int64_t residual_stride_m, void* residual_out,
+                                       int64_t residual_out_stride_m, const void* norm_weight,
+                                       float eps, const int8_t* w, int64_t w_stride_n,
+                                       const void* scale, int32_t scale_dtype, int32_t group_size,
+                                       const void* bias, void* y, int64_t y_stride_m, int64_t M,
+                                       int64_t N, int64_t K, int32_t dtype, void* stream) {
+  sd::clear_error();
+  if (!norm_weight || K % 8 != 0 || K > 8192) {
+    sd::set_error("w8a16_rmsnorm: needs the norm weight and K a multiple of 8 up to 8192 (K=%lld)",
+                  (long long)K);
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (residual && residual_out && (residual == residual_out || residual_out == x)) {
+    sd::set_error("w8a16_rmsnorm: residual_out may not alias the residual or x (other "
+                  "workgroups still read them)");
+    return SD_ERR_VALUE;
+  }
+  if ((residual && (!sd::aligned16(residual) || residual_stride_m % 8)) ||
+      (residual_out && (!sd::aligned16(residual_out) || residual_out_stride_m % 8)) ||
+      !sd::aligned16(norm_weight)) {
+    sd::set_error("w8a16_rmsnorm: residual, residual_out and norm weight rows 16-byte aligned");
+    return SD_ERR_UNSUPPORTED;
+  }
+  const NormArgs norm{norm_weight, residual, residual_stride_m, residual_out,
+                      residual_out_stride_m, eps};
+  return run_w8a16(x, x_stride_m, -1, norm, w, w_stride_n, scale, scale_dtype, group_size, bias, y,
+                   y_stride_m, M, N, K, dtype, stream);
 }

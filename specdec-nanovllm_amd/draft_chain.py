@@ -16,9 +16,12 @@ attention and the W8A16 linears of this library, and the next token is the
 argmax of the logits (the greedy draft). The hot-path ops run on the gfx950
 kernels. The neighbours of the path — RMSNorm (+ residual add), q/k norm +
 RoPE, SiLU*mul and the argmax — are plain eager torch (no torch.compile) with
-``fused=False``, or this library's fused neighbour kernels with ``fused=True``
-(q/k norm + RoPE in place on the qkv output, which the attention reads through
-strides; the embedding lookup stays a torch index).
+``fused=False``, or this library's fused neighbour kernels with ``fused=True``:
+add + RMSNorm inside the projection that consumes it (qkv, gate_up, lm_head;
+at up to 4 rows, two launches beyond), q/k norm + RoPE + store_kvcache in one
+launch on the qkv output (the attention reads q through strides), SiLU*mul
+inside the down projection, the sampler's argmax; the embedding lookup stays a
+torch index.
 
 ``chain()`` runs ``k`` steps back to back, each feeding its tokens to the next,
 on static buffers, so the whole chain can be captured in one HIP graph.
@@ -101,6 +104,9 @@ class DraftChain:
 
         # static token buffers: tokens[0] = the last context token, tokens[s+1] = step s output
         self.tokens = torch.randint(0, vocab, (k + 1, batch), generator=cg).to(self.dev)
+        # residual stream of the fused step: the norm fused into a projection
+        # writes x + residual to the buffer the current residual is not in
+        self._res = torch.empty((2, batch, hidden), device=self.dev, dtype=dtype)
 
     # ------------------------------------------------------------------ neighbours
     def _rms(self, x, w):
@@ -160,14 +166,17 @@ class DraftChain:
         B, Hq, Hkv, D, eps = self.B, self.Hq, self.Hkv, self.D, self.eps
         pos, slots, ctx = self.positions[s], self.slots[s], self.ctx[s]
         h = self.embed[self.tokens[s]]
-        residual = None
+        residual, ping = None, 0
         for li, lw in enumerate(self.layers):
+            # add + RMSNorm folded into the projection that consumes it
             if residual is None:
                 residual = h
-                x = ops.rmsnorm(h, lw["in_norm"], eps)
+                qkv = ops.w8a16_rmsnorm_linear(h, lw["in_norm"], eps, *lw["qkv"])
             else:
-                x, residual = ops.rmsnorm(h, lw["in_norm"], eps, residual=residual)
-            qkv = ops.w8a16_linear(x, *lw["qkv"])
+                ro, ping = self._res[ping], ping ^ 1
+                qkv = ops.w8a16_rmsnorm_linear(h, lw["in_norm"], eps, *lw["qkv"],
+                                               residual=residual, residual_out=ro)
+                residual = ro
             q = qkv[:, :Hq * D].view(B, Hq, D)
             kk = qkv[:, Hq * D:(Hq + Hkv) * D].view(B, Hkv, D)
             v = qkv[:, (Hq + Hkv) * D:].view(B, Hkv, D)
@@ -177,10 +186,13 @@ class DraftChain:
             o = ops.paged_attention(q, self.kv[0, li], self.kv[1, li], self.block_table,
                                     self.scale, context_lens=ctx)
             h = ops.w8a16_linear(o.reshape(B, Hq * D), *lw["o"])
-            x, residual = ops.rmsnorm(h, lw["post_norm"], eps, residual=residual)
-            h = ops.w8a16_silu_linear(ops.w8a16_linear(x, *lw["gate_up"]), *lw["down"])
-        x, _ = ops.rmsnorm(h, self.final_norm, eps, residual=residual)
-        logits = ops.w8a16_linear(x, *self.lm_head)
+            ro, ping = self._res[ping], ping ^ 1
+            gu = ops.w8a16_rmsnorm_linear(h, lw["post_norm"], eps, *lw["gate_up"],
+                                          residual=residual, residual_out=ro)
+            residual = ro
+            h = ops.w8a16_silu_linear(gu, *lw["down"])
+        logits = ops.w8a16_rmsnorm_linear(h, self.final_norm, eps, *self.lm_head,
+                                          residual=residual)
         ops.sample(logits, out=self.tokens[s + 1])
         return logits
 

@@ -182,3 +182,76 @@ def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
     two = ops.w8a16_linear(ops.silu_mul(gu), c["w"], s, bias, group_size=gs)
     assert torch.equal(fused, two)
     assert torch.equal(ops.w8a16_silu_linear(gu, c["w"], s, bias, group_size=gs), two)
+
+
+@pytest.mark.parametrize("M,N,K,gs,act,res", [(1, 4096, 1024, 0, torch.bfloat16, True),
+                                              (16, 6144, 1024, 0, torch.bfloat16, True),
+                                              (40, 1024, 1024, 0, torch.bfloat16, True),
+                                              (3, 512, 1152, 0, torch.float16, True),
+                                              (2, 1024, 8192, 0, torch.bfloat16, False),
+                                              (9, 33000, 1024, 128, torch.float16, True)])
+def test_rmsnorm_linear_is_rmsnorm_then_linear(M, N, K, gs, act, res):
+    # add + RMSNorm formed while staging: bit-identical to rmsnorm then the
+    # linear, residual_out identical to rmsnorm's (one row block per 16 or 32
+    # rows; K = 1152 leaves the last chunk column partly empty)
+    c = workloads.w8a16_case(M, N, K, seed=M + N + K, act_dtype=act)
+    g = workloads.device_generator(DEV, 19)
+    x = (torch.randn((M, K), generator=g, device=DEV) * 2).to(act)
+    r = (torch.randn((M, K), generator=g, device=DEV)).to(act) if res else None
+    nw = (1 + 0.1 * torch.randn((K,), generator=g, device=DEV)).to(act)
+    s = c["s"] if not gs else (torch.rand((N, K // gs), generator=g, device=DEV) * 3e-3 + 1e-3).to(act)
+    bias = torch.randn((N,), generator=g, device=DEV).to(act)
+    if res:
+        h, want_res = ops.rmsnorm(x, nw, 1e-6, residual=r)
+    else:
+        h, want_res = ops.rmsnorm(x, nw, 1e-6), None
+    two = ops.w8a16_linear(h, c["w"], s, bias, group_size=gs)
+    lib = _lib.load()
+    fused = torch.empty((M, N), dtype=act, device=DEV)
+    ro = torch.full((M, K), float("nan"), dtype=act, device=DEV) if res else None
+    rc = lib.sd_w8a16_rmsnorm_linear(
+        x.data_ptr(), x.stride(0), None if r is None else r.data_ptr(), K,
+        None if ro is None else ro.data_ptr(), K, nw.data_ptr(), 1e-6, c["w"].data_ptr(),
+        c["w"].stride(0), s.data_ptr(), _lib.dtype_code(s.dtype), gs, bias.data_ptr(),
+        fused.data_ptr(), fused.stride(0), M, N, K, _lib.dtype_code(act),
+        _lib.stream_ptr(torch.device(DEV)))
+    _lib.check(rc)
+    assert torch.equal(fused, two)
+    if res:
+        assert torch.equal(ro, want_res)
+        ro2 = torch.empty_like(ro)
+        assert torch.equal(ops.w8a16_rmsnorm_linear(x, nw, 1e-6, c["w"], s, bias, gs, residual=r,
+                                                    residual_out=ro2), two)
+        assert torch.equal(ro2, want_res)
+        # residual_out not wanted
+        assert torch.equal(ops.w8a16_rmsnorm_linear(x, nw, 1e-6, c["w"], s, bias, gs,
+                                                    residual=r), two)
+    else:
+        assert torch.equal(ops.w8a16_rmsnorm_linear(x, nw, 1e-6, c["w"], s, bias, gs), two)
+
+
+def test_rmsnorm_linear_falls_back_past_the_staging_lds():
+    # 16 rows of K = 4096 do not fit the staging LDS: the op runs rmsnorm and
+    # the linear (same results); the C entry reports the shape as unsupported
+    M, N, K = 16, 2048, 4096
+    c = workloads.w8a16_case(M, N, K, seed=5)
+    g = workloads.device_generator(DEV, 23)
+    x = torch.randn((M, K), generator=g, device=DEV).to(torch.bfloat16)
+    r = torch.randn((M, K), generator=g, device=DEV).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn((K,), generator=g, device=DEV)).to(torch.bfloat16)
+    h, want_res = ops.rmsnorm(x, nw, 1e-6, residual=r)
+    two = ops.w8a16_linear(h, c["w"], c["s"])
+    ro = torch.empty_like(x)
+    assert torch.equal(ops.w8a16_rmsnorm_linear(x, nw, 1e-6, c["w"], c["s"], residual=r,
+                                                residual_out=ro), two)
+    assert torch.equal(ro, want_res)
+
+
+def test_rmsnorm_linear_rejects_aliased_residual():
+    M, N, K = 2, 512, 1024
+    c = workloads.w8a16_case(M, N, K, seed=6)
+    x = torch.randn((M, K), device=DEV).to(torch.bfloat16)
+    r = torch.randn((M, K), device=DEV).to(torch.bfloat16)
+    nw = torch.ones((K,), device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="alias"):
+        ops.w8a16_rmsnorm_linear(x, nw, 1e-6, c["w"], c["s"], residual=r, residual_out=r)
