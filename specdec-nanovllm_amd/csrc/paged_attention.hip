@@ -9,19 +9,20 @@
 // nanovllm/engine/model_runner.py:522-533).
 //
 // Work decomposition (stream-K over keys, in columns):
-//   A "pair" is one (sequence b, kv head h); a "column" is 128 keys of one
-//   sequence (all kv heads), so sequence b has ceil(L_b / 128) columns. All
-//   columns are laid end to end (b major) and cut into R = nwg / Hkv runs of
-//   S = max(ceil(C / R), min_steps) columns; workgroup w takes head w % Hkv of
-//   run w / Hkv, one workgroup step per column. Every workgroup streams the
-//   same number of bytes whatever the length mix, with no host sync: each
-//   workgroup derives C and its start from context_lens itself (a wave-wide
-//   scan of the B lengths). The Hkv workgroups of a run are dispatched
-//   together and read the same key rows of their Hkv heads at the same time,
-//   so each stretch of a page (key rows of all heads side by side) is
-//   fetched from HBM by one burst of neighbouring requests instead of Hkv
-//   visits at unrelated times.
-//   step  : the 4 wave64s of a workgroup take 32 keys each. A wave loads the
+//   A "pair" is one (sequence b, kv head h); a "column" is 32 keys of one
+//   sequence (all kv heads), so sequence b has ceil(L_b / 32) columns. All
+//   columns are laid end to end (b major) and cut into R runs of
+//   S = max(ceil(C / R), min_steps) columns. A workgroup has NW wave64s (NW
+//   divides Hkv: 4, 2 or 1) and takes heads hg NW .. hg NW + NW - 1 of one run
+//   (workgroup w: run w / (Hkv / NW), head group w % (Hkv / NW)): wave i owns
+//   head hg NW + i, and all NW waves walk the same columns, so the workgroup
+//   reads NW adjacent 256-byte head rows (NW x 256 contiguous bytes) of every
+//   key instead of one. Every workgroup streams the same number of bytes
+//   whatever the length mix, with no host sync: each workgroup derives C and
+//   its start from context_lens itself (a wave-wide scan of the B lengths).
+//   The head groups of a run are dispatched together, so a stretch of a page
+//   (key rows of all heads side by side) is fetched by neighbouring requests.
+//   step  : each wave takes the column's 32 keys of its head. It loads the
 //           next step's K and V rows (16-byte loads) while it computes the
 //           current one (register double buffer), then per 32 keys
 //             S^T = K . Q^T      4 x MFMA 16x16x32 per 16 keys per row tile
@@ -30,12 +31,12 @@
 //                                16-bit parts), V^T gathered from LDS
 //           The S^T / O^T orientation puts one query row per lane (l % 16),
 //           so the softmax state never moves between lanes.
-//   flush : when a pair ends (or the run does) the four waves' (m, l, acc)
-//           meet in LDS. A pair covered by one workgroup is written out
-//           normalised; otherwise the workgroup writes a partial to slot
-//           (run + b) * Hkv + h of the workspace and `paged_attn_combine`
-//           merges the partials of each pair (that slot is unique: a later
-//           run can only meet a later sequence).
+//   flush : when a pair ends (or the run does) each wave writes its own head's
+//           state straight from registers (no LDS, no barrier): normalised
+//           rows if this run saw the whole pair, otherwise a partial to slot
+//           (run + b) * Hkv + h of the workspace, which `paged_attn_combine`
+//           merges per pair (that slot is unique: a later run can only meet a
+//           later sequence).
 // G * max_qlen query rows are padded to RT tiles of 16 rows (RT = 1: decode
 // with G <= 16 or the 0.6B verify; RT = 2: Qwen3-4B verify with 7 x 4 rows).
 //
@@ -55,10 +56,8 @@ using sd::f32x4;
 using sd::u32x4;
 
 constexpr int kD = 128;                // head_dim
-constexpr int kWaves = 4;              // wave64s per workgroup
-constexpr int kThreads = 256;
-constexpr int kStep = 32;              // keys per wave per workgroup step
-constexpr int kTile = kWaves * kStep;  // keys per workgroup step
+constexpr int kThreads = 256;          // combine kernel
+constexpr int kStep = 32;              // keys of a column: one workgroup step
 constexpr int kKPitch = 136;  // 16-bit elements per LDS row of a K tile (272 B: b128 reads of
                               // 16 consecutive rows hit distinct banks)
 constexpr int kVPitch = 144;  // same for a V tile (288 B: transpose reads of 4 x 4 rows hit
@@ -90,7 +89,8 @@ struct AttnParams {
   int64_t o_stok, o_shead;
   float* ws_ml;       // [slots][rmax][2]  (m in log2 units, l)
   float* ws_acc;      // [slots][rmax][kD] unnormalised
-  int32_t nwg;        // workgroups: runs * Hkv
+  int32_t nwg;        // workgroups: runs * (Hkv / NW)
+  int32_t runs;
   int32_t min_steps;  // lower bound of columns per run
   int32_t rmax;       // G * max_qlen
   // Fused store_kvcache (knew == NULL: none). Query row t's key/value row is
@@ -141,7 +141,7 @@ __device__ __forceinline__ int walk_keys_uniform(const AttnParams& p, int b) {
   return L;
 }
 
-__device__ __forceinline__ int steps_of(int L) { return (L + kTile - 1) / kTile; }
+__device__ __forceinline__ int steps_of(int L) { return (L + kStep - 1) / kStep; }
 
 template <bool STORE>
 __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b) {
@@ -269,12 +269,9 @@ __device__ __forceinline__ void store4(uint16_t* dst, f32x4 v, float s) {
   *reinterpret_cast<uint2*>(dst) = w;
 }
 
-template <int RT>
-constexpr int smem_bytes() {
-  constexpr int vtile = kWaves * kStep * (kKPitch + kVPitch) * 2;  // K and V tile per wave
-  constexpr int merge = kWaves * RT * 16 * (2 + kD) * 4;
-  return vtile > merge ? vtile : merge;
-}
+// LDS of the main kernel: one K and one V tile per wave.
+template <int NW>
+constexpr int smem_bytes() { return NW * kStep * (kKPitch + kVPitch) * 2; }
 
 // One wave's share of one workgroup step: 32 keys of K and of V, lane l
 // holding key 4 r + l/16, dims 8 (l%16) .. +8 of k[r] / v[r] — 16 lanes read one
@@ -292,21 +289,22 @@ struct StepRegs {
 template <int RT>
 constexpr int main_occupancy() { return RT == 1 ? 2 : 1; }
 
-template <typename T, int RT, bool ONE_PAGE, bool STORE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(main_occupancy<RT>())))
+template <typename T, int RT, bool ONE_PAGE, bool STORE, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(main_occupancy<RT>())))
 void paged_attn_main(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[smem_bytes<RT>()];
+  __shared__ __attribute__((aligned(16))) char smem[smem_bytes<NW>()];
 
   const int tid = threadIdx.x;
   // wave index held in an SGPR: page lookups and page bases stay scalar
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
 
-  // ---- this workgroup's kv head and run of columns [s0, s1)
-  const int h = static_cast<int>(blockIdx.x) % p.Hkv;
-  const int run = static_cast<int>(blockIdx.x) / p.Hkv;
+  // ---- this wave's kv head and the workgroup's run of columns [s0, s1)
+  const int groups = p.Hkv / NW;
+  const int h = static_cast<int>(blockIdx.x) % groups * NW + wave;
+  const int run = static_cast<int>(blockIdx.x) / groups;
   const int total = __builtin_amdgcn_readfirstlane(cols_before<STORE>(p, p.num_seqs));
-  const int S = max((total + p.nwg / p.Hkv - 1) / (p.nwg / p.Hkv), p.min_steps);
+  const int S = max((total + p.runs - 1) / p.runs, p.min_steps);
   const int s0 = run * S;
   if (s0 >= total) return;
   const int s1 = min(s0 + S, total);
@@ -357,11 +355,11 @@ void paged_attn_main(AttnParams p) {
     // wave-uniform by construction; readfirstlane lets the compiler prove it, so
     // the block-table lookup is a scalar load (lgkmcnt) and never waits on the
     // vector loads in flight
-    const int t0 = __builtin_amdgcn_readfirstlane(min(lj * kTile + wave * kStep, last));
+    const int t0 = __builtin_amdgcn_readfirstlane(min(lj * kStep, last));
     lb = __builtin_amdgcn_readfirstlane(lb);
     const int32_t* btrow = p.bt + static_cast<int64_t>(lb) * p.bt_stride;
     const int64_t hoff = static_cast<int64_t>(lh) * p.c_shead;
-    const bool used = real && lj * kTile + wave * kStep <= last;  // wave-uniform
+    const bool used = real && lj * kStep <= last;  // workgroup-uniform
     if constexpr (ONE_PAGE) {
       // scalar page base + 32-bit lane offsets (key rows of one page)
       const int64_t base = kv_row<true>(p, btrow, t0) + hoff;
@@ -390,8 +388,8 @@ void paged_attn_main(AttnParams p) {
   uint16_t* vl = kl + kStep * kKPitch;
 
   auto compute_step = [&](StepRegs& R, int cj) {
-    const int tb = cj * kTile + wave * kStep;
-    if (tb >= si.L) return;
+    const int tb = cj * kStep;
+    if (tb >= si.L) return;  // workgroup-uniform
     // ---- stage the 32 K and V rows of this step (row-major, padded pitch)
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -487,68 +485,31 @@ void paged_attn_main(AttnParams p) {
     sd::wave_lds_sync();  // every lane has read the tile before the next step overwrites it
   };
 
-  // Merge the four waves' state of the current pair in LDS and write it out:
-  // normalised rows if this workgroup saw the whole pair, else a partial.
+  // Write this wave's state of the current pair from registers: normalised
+  // rows if this run saw the whole pair, else a partial. Lane (lr, lg) holds
+  // row 16 rt + lr, dims 16 dt + 4 lg .. +4 of tile rt.
   auto flush = [&](bool complete) {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) l_run[rt] = sd::sum_over_groups(l_run[rt]);
-    __syncthreads();  // every wave is done with its V tile; reuse LDS
-    float* mm = reinterpret_cast<float*>(smem);
-    float* ml = mm + kWaves * RT * 16;
-    float* ma = ml + kWaves * RT * 16;
+    const int64_t wslot = (static_cast<int64_t>(run) + b) * p.Hkv + h;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
+      const float l = sd::sum_over_groups(l_run[rt]);
       const int row = rt * 16 + lr;
-      const int slot = wave * RT * 16 + row;
-      if (lg == 0) {
-        mm[slot] = m_run[rt];
-        ml[slot] = l_run[rt];
-      }
-      if (row < si.R) {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-          sd::store16(ma + slot * kD + dt * 16 + lg * 4, __builtin_bit_cast(u32x4, acc[rt][dt]));
-      }
-    }
-    __syncthreads();
-    const int nrows = min(si.R, RT * 16);
-    const int64_t wslot = (static_cast<int64_t>(run) + b) * p.Hkv + h;
-    for (int idx = tid; idx < nrows * 32; idx += kThreads) {
-      const int row = idx >> 5, d4 = (idx & 31) * 4;
       const int qi = row / p.G, g = row - qi * p.G;
       const int64_t qt = si.q0 + qi;
-      if (qt < 0 || qt >= p.total_q) continue;
-      float mw[kWaves];
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        mw[w] = mm[w * RT * 16 + row];
-        M = fmaxf(M, mw[w]);
-      }
-      f32x4 o = {0.f, 0.f, 0.f, 0.f};
-      float l = 0.f;
-      if (M != -INFINITY) {
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-          const float e = exp2f(mw[w] - M);
-          l += e * ml[w * RT * 16 + row];
-          o += e * __builtin_bit_cast(f32x4, sd::load16(ma + (w * RT * 16 + row) * kD + d4));
-        }
-      }
+      if (row >= si.R || qt < 0 || qt >= p.total_q) continue;
       if (complete) {
-        uint16_t* op =
-            p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + d4;
-        store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);
+        uint16_t* op = p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + lg * 4;
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) store4<T>(op + dt * 16, acc[rt][dt], inv);
       } else {
         const int64_t e = wslot * p.rmax + row;
-        sd::store16(p.ws_acc + e * kD + d4, __builtin_bit_cast(u32x4, o));
-        if ((idx & 31) == 0) {
-          p.ws_ml[2 * e] = M;
-          p.ws_ml[2 * e + 1] = l;
-        }
+        float* ap = p.ws_acc + e * kD + lg * 4;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) sd::store16(ap + dt * 16, __builtin_bit_cast(u32x4, acc[rt][dt]));
+        if (lg == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * e) = make_float2(m_run[rt], l);
       }
     }
-    __syncthreads();  // LDS is V tiles again
   };
 
   // ---- walk [s0, s1): load step s + 1 while computing step s
@@ -634,8 +595,7 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
   float l = 0.f;
   if (n > 0) {
-    const int runs = p.nwg / p.Hkv;
-    const int S = max((total + runs - 1) / runs, p.min_steps);
+    const int S = max((total + p.runs - 1) / p.runs, p.min_steps);
     const int w0 = f / S, w1 = (f + n - 1) / S;
     if (!STORE && w0 == w1) return;
     const float2* ml = reinterpret_cast<const float2*>(p.ws_ml);
@@ -737,7 +697,9 @@ __global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
 // ------------------------------------------------------------------ host
 struct Plan {
   int RT;         // 16-row tiles of query rows
-  int nwg;        // workgroups of the main grid: runs * Hkv
+  int NW;         // waves (= kv heads) per main workgroup
+  int runs;
+  int nwg;        // workgroups of the main grid: runs * Hkv / NW
   int min_steps;  // lower bound of columns per run
   int rmax;       // rows per (sequence, kv head) in the workspace
   int64_t slots;  // partial slots: (runs + num_seqs) * Hkv
@@ -757,26 +719,31 @@ int device_cus() {
   return n;
 }
 
-// num_splits == 0: one resident set of workgroups (main_occupancy per compute
-// unit) shares all the steps.
-// num_splits > 0: num_splits workgroups per (sequence, kv head) on average,
-// the meaning of the reference's `splits` (KV splits per sequence).
+// num_splits == 0: one resident set of waves (4 SIMDs x main_occupancy per
+// compute unit, one wave per kv head of a run) shares all the columns, at
+// least 128 keys (256 for two row tiles) per run.
+// num_splits > 0: num_splits runs per sequence on average, the meaning of the
+// reference's `splits` (KV splits per sequence).
 Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   Plan pl;
   const int G = Hq / Hkv;
   pl.rmax = G * max_qlen;
   pl.RT = pl.rmax <= 16 ? 1 : 2;
+  pl.NW = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
   int64_t runs;
   if (num_splits > 0) {
     runs = static_cast<int64_t>(num_splits) * num_seqs;
     pl.min_steps = 1;
   } else {
-    runs = device_cus() * (pl.RT == 1 ? main_occupancy<1>() : main_occupancy<2>()) / Hkv;
-    pl.min_steps = pl.RT == 1 ? 1 : 2;
+    const int occ = pl.RT == 1 ? main_occupancy<1>() : main_occupancy<2>();
+    runs = static_cast<int64_t>(device_cus()) * 4 * occ / Hkv;
+    pl.min_steps = pl.RT == 1 ? 4 : 8;
   }
-  const int64_t cap = (1 << 20) / Hkv > 1 ? (1 << 20) / Hkv : 1;  // grid of at most ~2^20
+  const int groups = Hkv / pl.NW;
+  const int64_t cap = (1 << 20) / groups > 1 ? (1 << 20) / groups : 1;  // grid of at most 2^20
   runs = runs < 1 ? 1 : (runs > cap ? cap : runs);
-  pl.nwg = static_cast<int>(runs * Hkv);
+  pl.runs = static_cast<int>(runs);
+  pl.nwg = static_cast<int>(runs * groups);
   pl.slots = (runs + num_seqs) * Hkv;
   return pl;
 }
@@ -789,24 +756,33 @@ size_t ws_bytes(const Plan& pl) {
   return ml_bytes(pl) + static_cast<size_t>(pl.slots) * pl.rmax * kD * sizeof(float);
 }
 
-template <typename T, int RT, bool STORE>
+template <typename T, int RT, bool STORE, int NW>
 void launch_main(const AttnParams& p, hipStream_t st) {
   if (p.block_size % kStep == 0)
-    hipLaunchKernelGGL((paged_attn_main<T, RT, true, STORE>), dim3(p.nwg), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((paged_attn_main<T, RT, true, STORE, NW>), dim3(p.nwg), dim3(NW * 64), 0,
+                       st, p);
   else
-    hipLaunchKernelGGL((paged_attn_main<T, RT, false, STORE>), dim3(p.nwg), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((paged_attn_main<T, RT, false, STORE, NW>), dim3(p.nwg), dim3(NW * 64), 0,
+                       st, p);
+}
+
+template <typename T, int RT, bool STORE>
+void launch_main(const AttnParams& p, int NW, hipStream_t st) {
+  if (NW == 4) launch_main<T, RT, STORE, 4>(p, st);
+  else if (NW == 2) launch_main<T, RT, STORE, 2>(p, st);
+  else launch_main<T, RT, STORE, 1>(p, st);
 }
 
 template <typename T, int RT>
-void launch_main(const AttnParams& p, hipStream_t st) {
-  if (p.knew) launch_main<T, RT, true>(p, st);
-  else launch_main<T, RT, false>(p, st);
+void launch_main(const AttnParams& p, int NW, hipStream_t st) {
+  if (p.knew) launch_main<T, RT, true>(p, NW, st);
+  else launch_main<T, RT, false>(p, NW, st);
 }
 
 template <typename T>
 int launch_all(const AttnParams& p, const Plan& pl, bool combine, hipStream_t st) {
-  if (pl.RT == 1) launch_main<T, 1>(p, st);
-  else launch_main<T, 2>(p, st);
+  if (pl.RT == 1) launch_main<T, 1>(p, pl.NW, st);
+  else launch_main<T, 2>(p, pl.NW, st);
   int rc = sd::check_launch("paged_attention main");
   if (rc != SD_OK || !combine) return rc;
   const dim3 grid((pl.rmax + kThreads / 32 - 1) / (kThreads / 32), p.Hkv, p.num_seqs);
@@ -897,7 +873,7 @@ int run_attention(bool combine, const NewRows& nr, const void* q, int64_t q_stri
                   "at most 2^25 elements");
     return SD_ERR_UNSUPPORTED;
   }
-  if (static_cast<int64_t>(num_seqs) * num_kv_heads * ((max_ctx + kTile - 1) / kTile) >
+  if (static_cast<int64_t>(num_seqs) * num_kv_heads * ((max_ctx + kStep - 1) / kStep) >
       (1ll << 30)) {
     sd::set_error("paged_attention: %d sequences x %d kv heads x %lld keys is too much work "
                   "for one call", num_seqs, num_kv_heads, (long long)max_ctx);
@@ -942,6 +918,7 @@ int run_attention(bool combine, const NewRows& nr, const void* q, int64_t q_stri
   p.ws_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + ml_bytes(pl));
   p.num_seqs = num_seqs;
   p.nwg = pl.nwg;
+  p.runs = pl.runs;
   p.min_steps = pl.min_steps;
   p.knew = static_cast<const uint16_t*>(nr.key);
   p.vnew = static_cast<const uint16_t*>(nr.value);

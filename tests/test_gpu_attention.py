@@ -427,6 +427,7 @@ def test_mirror_entry_points_agree():
     # Attention module, decode branch (store then attend)
     attn = Attention(32, 128, 128 ** -0.5, 8)
     attn.k_cache, attn.v_cache = kc, vc
+    kc0 = kc.clone()
     knew = torch.randn((3, 8, 128), device=DEV).to(torch.bfloat16)
     slots = torch.full((3,), -1, dtype=torch.int32, device=DEV)  # no write: compare to base
     set_context(False, slot_mapping=slots, context_lens=ld, block_tables=btd)
@@ -434,7 +435,10 @@ def test_mirror_entry_points_agree():
         o = attn(q, knew, knew)
     finally:
         reset_context()
-    assert o.shape == (3, 1, 32, 128) and torch.equal(o[:, 0], base)
+    # the fused store scores the last key in the merge launch: equal up to rounding
+    assert o.shape == (3, 1, 32, 128)
+    assert_close_attn(to_np(o[:, 0]), to_np(base), what="Attention decode (fused store)")
+    assert torch.equal(kc, kc0)
 
 
 def test_attention_module_verify_branch():
