@@ -721,7 +721,7 @@ int device_cus() {
 
 // num_splits == 0: one resident set of waves (4 SIMDs x main_occupancy per
 // compute unit, one wave per kv head of a run) shares all the columns, at
-// least 128 keys (256 for two row tiles) per run.
+// least one column (two for two row tiles) per run.
 // num_splits > 0: num_splits runs per sequence on average, the meaning of the
 // reference's `splits` (KV splits per sequence).
 Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
@@ -737,7 +737,7 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   } else {
     const int occ = pl.RT == 1 ? main_occupancy<1>() : main_occupancy<2>();
     runs = static_cast<int64_t>(device_cus()) * 4 * occ / Hkv;
-    pl.min_steps = pl.RT == 1 ? 4 : 8;
+    pl.min_steps = pl.RT == 1 ? 1 : 2;
   }
   const int groups = Hkv / pl.NW;
   const int64_t cap = (1 << 20) / groups > 1 ? (1 << 20) / groups : 1;  // grid of at most 2^20
