@@ -176,8 +176,75 @@ def cpu_baseline(case, seconds, torch):
                       f"({spent:.1f} s, {threads} BLAS threads, os.cpu_count()={os.cpu_count()})"}
 
 
+def _blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        return 1
+
+
+def cpu_baseline_verify(case, seconds):
+    """numpy oracle (float32) over whole sequences of the C3 verify case (7
+    causal rows each) for about ``seconds``; GB/s on the same algorithmic bytes."""
+    import numpy as np
+    from oracle import paged_attention as opa
+    bt, keys, k = case["table"], case["keys"].tolist(), case["k"] + 1
+    q = case["q"].float().cpu().numpy()
+    host, done, spent, seqs, b = {}, 0, 0.0, 0, 0
+    while spent < seconds and seqs < 100000:
+        L = keys[b]
+        if b not in host:
+            pages = bt[b, :math.ceil(L / 256)].long().to(case["k_cache"].device)
+            host[b] = (case["k_cache"][pages].float().cpu().numpy(),
+                       case["v_cache"][pages].float().cpu().numpy(),
+                       np.arange(len(pages)).reshape(1, -1))
+        kc, vc, table = host[b]
+        t0 = time.perf_counter()
+        opa.paged_attention(q[b * k:(b + 1) * k], kc, vc, table, [L], case["scale"],
+                            np.array([0, k]), dtype=np.float32)
+        spent += time.perf_counter() - t0
+        done += attn_bytes([L], 32, 8, 128, 2, q_rows=k)
+        seqs += 1
+        b = (b + 1) % len(keys)
+    threads = _blas_threads()
+    return {"value": round(done / spent / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"numpy fp32 oracle, {seqs} whole sequences of C3 (7 causal rows each, "
+                      f"{spent:.1f} s, {threads} BLAS threads)"}
+
+
+def cpu_baseline_w8a16(seconds):
+    """numpy oracle (float32 dequantize, then matmul) of the C4 lm_head shape
+    (N 151936, K 1024) at M = 1 and M = 16 on row slices of the weight, about
+    ``seconds`` in all; GB/s on the algorithmic bytes of the rows done."""
+    import numpy as np
+    from oracle import w8a16 as ow8
+    rng = np.random.default_rng(0)
+    N, K, rows = 151936, 1024, 8192
+    w = np.clip(np.round(rng.standard_normal((rows, K)) * 40), -127, 127).astype(np.int8)
+    s = (rng.random(rows) * 3e-3 + 1e-3).astype(np.float32)
+    out = {}
+    for M in (1, 16):
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        done, spent, calls = 0, 0.0, 0
+        while spent < seconds / 2 and calls < 100000:
+            t0 = time.perf_counter()
+            ow8.int8_linear(x, w, s, dtype=np.float32)
+            spent += time.perf_counter() - t0
+            done += ow8.algorithmic_bytes(M, rows, K)
+            calls += 1
+        out[f"M{M}"] = {"GBps": round(done / spent / 1e9, 3),
+                        "us_full_lm_head": round(spent / calls * N / rows * 1e6, 1)}
+    threads = _blas_threads()
+    return {"value": out["M1"]["GBps"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "by_M": out,
+            "sample": f"numpy fp32 oracle (dequantize then matmul), lm_head K=1024 on "
+                      f"{rows}-row slices, M=1 and M=16, {seconds:.0f} s, {threads} BLAS threads"}
+
+
 # ----------------------------------------------------------------------------- extras
-def bench_verify(ops, workloads, torch, steps):
+def bench_verify(ops, workloads, torch, steps, cpu_seconds=0.0):
     case = workloads.verify_case(seed=0)
     dev = "cuda"
     bt, cuq, cuk = case["table"].to(dev), case["cu_q"].to(dev), case["cu_k"].to(dev)
@@ -192,9 +259,12 @@ def bench_verify(ops, workloads, torch, steps):
     nbytes = (attn_bytes(case["keys"].tolist(), 32, 8, 128, 2, q_rows=case["k"] + 1)
               + case["slots"].numel() * 8 * 128 * 2 * 2 * 2)
     flops = sum(4 * 32 * 128 * (case["k"] + 1) * int(L) for L in case["keys"])
-    return {"config": "C3 verify B=8 q_len 7 (store + attention)", "us": round(ms * 1e3, 2),
-            "GBps": round(nbytes / ms / 1e6, 1), "TFLOPs": round(flops / ms / 1e9, 2),
-            "seed": case["seed_used"]}
+    res = {"config": "C3 verify B=8 q_len 7 (store + attention)", "us": round(ms * 1e3, 2),
+           "GBps": round(nbytes / ms / 1e6, 1), "TFLOPs": round(flops / ms / 1e9, 2),
+           "seed": case["seed_used"]}
+    if cpu_seconds > 0:
+        res["cpu_baseline"] = cpu_baseline_verify(case, cpu_seconds)
+    return res
 
 
 def bench_w8a16(ops, workloads, torch, steps):
@@ -456,9 +526,12 @@ def main():
                  "step_us_one_graph_per_step": round(ms_step_graph * 1e3, 2)}
         del case, kc, vc
         torch.cuda.empty_cache()
-        extra["verify"] = bench_verify(ops, workloads, torch, args.steps)
+        cpu_s = 0.0 if args.no_cpu_baseline else max(args.cpu_seconds / 2, 1.0)
+        extra["verify"] = bench_verify(ops, workloads, torch, args.steps, cpu_s)
         torch.cuda.empty_cache()
         extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100))
+        if cpu_s > 0:
+            extra["w8a16_cpu_baseline"] = cpu_baseline_w8a16(cpu_s)
         torch.cuda.empty_cache()
         extra["verify_batch"] = bench_verify_batch(ops, torch, min(args.steps, 100))
         torch.cuda.empty_cache()
