@@ -92,6 +92,7 @@ struct AttnParams {
   int32_t nwg;        // workgroups: runs * (Hkv / NW)
   int32_t runs;
   int32_t min_steps;  // lower bound of columns per run
+  int32_t comb_rows;  // query rows per combine workgroup (a power of two <= 8)
   int32_t rmax;       // G * max_qlen
   // Fused store_kvcache (knew == NULL: none). Query row t's key/value row is
   // knew/vnew row t; sequence b's rows are its last n_b keys.
@@ -562,99 +563,162 @@ __device__ __forceinline__ f32x4 load4f(const uint16_t* src) {
                sd::from_bits<T>(static_cast<uint16_t>(w.y)), sd::from_bits<T>(static_cast<uint16_t>(w.y >> 16))};
 }
 
+// Wave-wide: the columns of sequences [0, b) and of all sequences, one pass.
+template <bool STORE>
+__device__ void cols_split(const AttnParams& p, int b, int& before, int& total) {
+  const int lane = threadIdx.x & 63;
+  int sb = 0, st = 0;
+  for (int c = 0; c < p.num_seqs; c += 64) {
+    const int s = c + lane;
+    const int n = s < p.num_seqs ? steps_of(walk_keys<STORE>(p, s)) : 0;
+    st += n;
+    sb += s < b ? n : 0;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    st += __shfl_xor(st, off);
+    sb += __shfl_xor(sb, off);
+  }
+  before = sb;
+  total = st;
+}
+
 // Log-sum-exp merge of the partials of pair (b, h) = (blockIdx.z, blockIdx.y),
-// rows blockIdx.x * 8 .. +8 (one thread per row and 4 dims), zero rows for
-// sequences without keys. Sequence b spans columns [f, f + n); the runs
-// that met it are f / S .. (f + n - 1) / S and run r's workgroup of head h
-// wrote its partial to slot (r + b) * Hkv + h. Without STORE a pair met by one
-// run is already final. STORE: every run wrote a partial of the cached keys,
-// and the sequence's n_b new keys (new row j at position L - n_b + j, seen by
-// query rows qi >= j) are merged here: s_j = q . k_j from the 16-bit inputs in
-// fp32, k_j / v_j from key / value — or from the cache row when the row's slot
-// is not stored (-1 or outside the pool), as an unfused store would leave it.
+// rows blockIdx.x * rpw .. + rpw (rpw = comb_rows, a power of two <= 8), zero
+// rows for sequences without keys. The 8 groups of 32 threads (4 dims per
+// thread) are rpw rows x 8 / rpw slices: slice s of a row merges its own
+// contiguous share of the row's partials, all loads of a batch in flight at
+// once, then slice 0 merges the slices' states (LDS) in slice order. Sequence
+// b spans columns [f, f + n); the runs that met it are f / S .. (f + n - 1) / S
+// and run r's wave of head h wrote its partial to slot
+// (r + b) * Hkv + h. Without STORE a pair met by one run is already final.
+// STORE: every run wrote a partial of the cached keys, and the sequence's n_b
+// new keys (new row j at position L - n_b + j, seen by query rows qi >= j) are
+// merged last: s_j = q . k_j from the 16-bit inputs in fp32, k_j / v_j from
+// key / value — or from the cache row when the row's slot is not stored (-1
+// or outside the pool), as an unfused store would leave it. Their loads are
+// issued first, beside the scan of the lengths.
 template <typename T, bool STORE>
 __device__ __forceinline__ void combine_rows(const AttnParams& p) {
-  constexpr int kUnroll = 16;
+  constexpr int kBatch = 16;   // partial loads in flight per thread
+  constexpr int kNewMax = 8;   // new rows whose loads are issued up front
+  constexpr int kGroups = kThreads / 32;
+  __shared__ __attribute__((aligned(16))) float4 s_o[kGroups][32];
+  __shared__ float2 s_ml[kGroups];
   const int h = blockIdx.y, b = blockIdx.z;
   const SeqInfo si = seq_info<STORE>(p, b);
-  const int row = blockIdx.x * (kThreads / 32) + (threadIdx.x >> 5);
-  const int d4 = (threadIdx.x & 31) * 4;
-  const int total = cols_before<STORE>(p, p.num_seqs);
-  const int f = cols_before<STORE>(p, b);
-  if (row >= si.R) return;
+  const int grp = threadIdx.x >> 5, d4 = (threadIdx.x & 31) * 4;
+  const int rpw = p.comb_rows, nsl = kGroups / rpw;
+  const int sl = grp / rpw;
+  const int row = blockIdx.x * rpw + grp % rpw;
   const int qi = row / p.G, g = row - qi * p.G;
   const int64_t qt = si.q0 + qi;
-  if (qt < 0 || qt >= p.total_q) return;
-  uint16_t* op = p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + d4;
+  const bool live = row < si.R && qt >= 0 && qt < p.total_q;
   const int n = steps_of(si.L);
-  if (!STORE && n == 0) {
-    *reinterpret_cast<uint2*>(op) = make_uint2(0u, 0u);
-    return;
-  }
-  float M = -INFINITY;
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  float l = 0.f;
-  if (n > 0) {
-    const int S = max((total + p.runs - 1) / p.runs, p.min_steps);
-    const int w0 = f / S, w1 = (f + n - 1) / S;
-    if (!STORE && w0 == w1) return;
-    const float2* ml = reinterpret_cast<const float2*>(p.ws_ml);
-    const int64_t base = ((static_cast<int64_t>(w0) + b) * p.Hkv + h) * p.rmax + row;
-    const int64_t run_stride = static_cast<int64_t>(p.Hkv) * p.rmax;  // rows between runs
-    const int cnt = w1 - w0 + 1;
-    for (int c0 = 0; c0 < cnt; c0 += kUnroll) {
-      float2 part[kUnroll];
-      f32x4 a[kUnroll];
+
+  // STORE: the new rows' key / value / slot and this row's q, loaded now
+  f32x4 qv = {0.f, 0.f, 0.f, 0.f}, kn[kNewMax], vn[kNewMax];
+  int64_t sn[kNewMax];
+  if constexpr (STORE) {
+    if (live && sl == 0) {
+      qv = load4f<T>(p.q + qt * p.q_stok + static_cast<int64_t>(h * p.G + g) * p.q_shead + d4);
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int64_t e = base + static_cast<int64_t>(c0 + u) * run_stride;
-        if (c0 + u < cnt) {
-          part[u] = ml[e];
-          a[u] = __builtin_bit_cast(f32x4, sd::load16(p.ws_acc + e * kD + d4));
-        } else {
-          part[u] = make_float2(-INFINITY, 0.f);
-          a[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < kNewMax; ++j) {
+        if (j < si.nq && j <= qi) {
+          const int64_t tr = si.q0 + j;
+          sn[j] = p.slot[tr];
+          kn[j] = load4f<T>(p.knew + tr * p.kn_stok + static_cast<int64_t>(h) * p.kn_shead + d4);
+          vn[j] = load4f<T>(p.vnew + tr * p.vn_stok + static_cast<int64_t>(h) * p.vn_shead + d4);
         }
       }
-      float mc = M;
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) mc = fmaxf(mc, part[u].x);
-      if (mc == -INFINITY) continue;
-      const float r = exp2f(M - mc);  // rescale what earlier batches summed
-      l *= r;
-      o *= r;
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const float w = exp2f(part[u].x - mc);
-        l += w * part[u].y;
-        o += w * a[u];
-      }
-      M = mc;
     }
+  }
+
+  int f, total;
+  cols_split<STORE>(p, b, f, total);
+  float M = -INFINITY, l = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  bool final_by_main = !STORE && n == 0;  // (zeros written below)
+  if (live && n > 0) {
+    const int S = max((total + p.runs - 1) / p.runs, p.min_steps);
+    const int w0 = f / S, w1 = (f + n - 1) / S;
+    if (!STORE && w0 == w1) final_by_main = true;
+    if (!final_by_main) {
+      const int cnt = w1 - w0 + 1;
+      const int per = (cnt + nsl - 1) / nsl;
+      const int u0 = sl * per, u1 = min(u0 + per, cnt);
+      const float2* ml = reinterpret_cast<const float2*>(p.ws_ml);
+      const int64_t base = ((static_cast<int64_t>(w0) + b) * p.Hkv + h) * p.rmax + row;
+      const int64_t run_stride = static_cast<int64_t>(p.Hkv) * p.rmax;  // rows between runs
+      for (int c0 = u0; c0 < u1; c0 += kBatch) {
+        float2 part[kBatch];
+        f32x4 a[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int64_t e = base + static_cast<int64_t>(c0 + u) * run_stride;
+          if (c0 + u < u1) {
+            part[u] = ml[e];
+            a[u] = __builtin_bit_cast(f32x4, sd::load16(p.ws_acc + e * kD + d4));
+          } else {
+            part[u] = make_float2(-INFINITY, 0.f);
+            a[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+        float mc = M;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) mc = fmaxf(mc, part[u].x);
+        if (mc == -INFINITY) continue;
+        const float r = exp2f(M - mc);  // rescale what earlier batches summed
+        l *= r;
+        o *= r;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const float w = exp2f(part[u].x - mc);
+          l += w * part[u].y;
+          o += w * a[u];
+        }
+        M = mc;
+      }
+    }
+  }
+  if (nsl > 1) {  // workgroup-uniform
+    s_o[grp][threadIdx.x & 31] = make_float4(o.x, o.y, o.z, o.w);
+    if ((threadIdx.x & 31) == 0) s_ml[grp] = make_float2(M, l);
+    __syncthreads();
+    if (sl == 0) {
+      float mc = M;
+      for (int s2 = 1; s2 < nsl; ++s2) mc = fmaxf(mc, s_ml[s2 * rpw + grp].x);
+      if (mc != -INFINITY) {
+        const float r = exp2f(M - mc);
+        l *= r;
+        o *= r;
+        for (int s2 = 1; s2 < nsl; ++s2) {
+          const float2 pm = s_ml[s2 * rpw + grp];
+          const float4 po = s_o[s2 * rpw + grp][threadIdx.x & 31];
+          const float w = exp2f(pm.x - mc);
+          l += w * pm.y;
+          o += w * f32x4{po.x, po.y, po.z, po.w};
+        }
+        M = mc;
+      }
+    }
+  }
+  if (!live || sl != 0) return;
+  uint16_t* op = p.out + qt * p.o_stok + static_cast<int64_t>(h * p.G + g) * p.o_shead + d4;
+  if (final_by_main) {
+    if (n == 0) *reinterpret_cast<uint2*>(op) = make_uint2(0u, 0u);
+    return;
   }
   if constexpr (STORE) {
     // the 32 lanes of this row hold 4 dims each; the dot products reduce over them
     const int L = seq_keys(p, b);
-    const f32x4 qv =
-        load4f<T>(p.q + qt * p.q_stok + static_cast<int64_t>(h * p.G + g) * p.q_shead + d4);
     const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
-    for (int j = 0; j < si.nq; ++j) {  // uniform over the row's lanes
-      const int pos = L - si.nq + j;
-      if (pos < 0 || j > qi) continue;
-      const int64_t tr = si.q0 + j;
-      const int64_t slot = p.slot[tr];
-      const uint16_t* kr;
-      const uint16_t* vr;
-      if (slot >= 0 && slot < p.num_slots) {
-        kr = p.knew + tr * p.kn_stok + static_cast<int64_t>(h) * p.kn_shead;
-        vr = p.vnew + tr * p.vn_stok + static_cast<int64_t>(h) * p.vn_shead;
-      } else {
-        const int64_t crow = kv_row(p, btrow, pos) + static_cast<int64_t>(h) * p.c_shead;
-        kr = p.kc + crow;
-        vr = p.vc + crow;
+    auto merge_new = [&](int j, f32x4 kv, f32x4 vv, int64_t slot) {
+      if (!(slot >= 0 && slot < p.num_slots)) {  // not stored: the cache row stays
+        const int64_t crow = kv_row(p, btrow, L - si.nq + j) + static_cast<int64_t>(h) * p.c_shead;
+        kv = load4f<T>(p.kc + crow + d4);
+        vv = load4f<T>(p.vc + crow + d4);
       }
-      const f32x4 kv = load4f<T>(kr + d4);
-      const f32x4 vv = load4f<T>(vr + d4);
       float dot = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
 #pragma unroll
       for (int off = 1; off < 32; off <<= 1) dot += __shfl_xor(dot, off);
@@ -664,6 +728,20 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
       l = l * r + w;
       o = o * r + w * vv;
       M = mn;
+    };
+#pragma unroll
+    for (int j = 0; j < kNewMax; ++j) {  // uniform over the row's lanes
+      if (j >= si.nq) break;
+      if (L - si.nq + j < 0 || j > qi) continue;
+      merge_new(j, kn[j], vn[j], sn[j]);
+    }
+    for (int j = kNewMax; j < si.nq; ++j) {
+      if (L - si.nq + j < 0 || j > qi) continue;
+      const int64_t tr = si.q0 + j;
+      merge_new(j,
+                load4f<T>(p.knew + tr * p.kn_stok + static_cast<int64_t>(h) * p.kn_shead + d4),
+                load4f<T>(p.vnew + tr * p.vn_stok + static_cast<int64_t>(h) * p.vn_shead + d4),
+                p.slot[tr]);
     }
   }
   store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);
@@ -785,7 +863,7 @@ int launch_all(const AttnParams& p, const Plan& pl, bool combine, hipStream_t st
   else launch_main<T, 2>(p, pl.NW, st);
   int rc = sd::check_launch("paged_attention main");
   if (rc != SD_OK || !combine) return rc;
-  const dim3 grid((pl.rmax + kThreads / 32 - 1) / (kThreads / 32), p.Hkv, p.num_seqs);
+  const dim3 grid((pl.rmax + p.comb_rows - 1) / p.comb_rows, p.Hkv, p.num_seqs);
   if (p.knew)
     hipLaunchKernelGGL((paged_attn_combine<T, true>), grid, dim3(kThreads), 0, st, p);
   else
@@ -920,6 +998,10 @@ int run_attention(bool combine, const NewRows& nr, const void* q, int64_t q_stri
   p.nwg = pl.nwg;
   p.runs = pl.runs;
   p.min_steps = pl.min_steps;
+  // rows per combine workgroup: few rows (decode) leave groups free to split
+  // each row's partials
+  p.comb_rows = 1;
+  while (p.comb_rows < 8 && p.comb_rows < pl.rmax) p.comb_rows *= 2;
   p.knew = static_cast<const uint16_t*>(nr.key);
   p.vnew = static_cast<const uint16_t*>(nr.value);
   p.kn_stok = nr.key_stride_tok;
