@@ -175,9 +175,10 @@ def test_fp16():
     assert_close_attn(to_np(out), oracle(q, kc, vc, bt, lens, 128 ** -0.5), what="fp16")
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8), (12, 3)])
 def test_verify_ragged_rows(hq, hkv):
-    # rows per sequence 1..7; one sequence has fewer keys than rows
+    # rows per sequence 1..7; one sequence has fewer keys than rows. 32/8 puts the
+    # two row tiles on two waves; 12/3 (odd kv heads) keeps both tiles on one wave
     nq = [1, 7, 3, 5, 7, 4]
     keys = [900, 2600, 3, 257, 1, 40]
     lens = torch.tensor(keys, dtype=torch.int32)
