@@ -20,7 +20,9 @@
 // resident workgroups walks the row groups (16 NT rows) grid-stride; a row
 // group is either one wave's (whole K, when rows are plentiful) or shared by
 // the four waves of a workgroup that split K and add their partials in LDS
-// (narrow layers such as N = 1024).
+// (narrow layers such as N = 1024). One or two activation rows on matrices up
+// to 32 MiB take the row-streaming kernel instead (w8a16_rows_kernel: whole
+// weight rows per load, activations in registers, no MFMA or LDS).
 //
 // int8 -> fp16: (b ^ 0x80) in the low byte under exponent byte 0x64 is the
 // fp16 value 1024 + b + 128, exact; subtracting 1152 (packed fp16) gives b.
@@ -475,6 +477,215 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
   }
 }
 
+// ---- row-streaming GEMV for one or two activation rows (decode)
+// Each wave owns a contiguous range of weight rows and streams them whole: a
+// load instruction moves 1 KB of one row (lane l: bytes 16 l .. +16 of each
+// 1024-column chunk), R rows per batch, two batches in flight. Lane l holds
+// the activations of its columns (MR rows x C chunks x 16) in registers for
+// the whole launch, formed once per wave: MODE 1 SiluAndMul (silu_mul8, the
+// SiLU kernel's element function), MODE 2 add + RMSNorm with the RMSNorm
+// kernel's summation order (below), so the fused forms equal their two-launch
+// forms bit for bit. Products accumulate in fp32 per lane (one conversion and
+// one FMA per weight), then the R x MR sums of a batch reduce across the
+// lanes in one reduce-scatter (halving steps, then plain xor steps), so a
+// row's result is always summed in the same order. No MFMA, no LDS: at one or
+// two rows the MFMA form spends its time on operand staging, not on math.
+// Per group (PG): lane l's 16 columns of chunk c lie in one group; its partial
+// is scaled before the reduction.
+template <int MR, int C, int R>
+struct RowsShape {
+  static constexpr int V = R * MR;  // sums per lane per batch
+  static constexpr int LV = V == 16 ? 4 : (V == 8 ? 3 : (V == 4 ? 2 : (V == 2 ? 1 : 0)));
+  static_assert((1 << LV) == V, "R * MR must be a power of two <= 16");
+};
+
+template <typename T, int MR, int C, int R, int MODE, bool PG>
+__global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int rows_per_wave) {
+#pragma clang fp contract(off)
+  constexpr int V = RowsShape<MR, C, R>::V, LV = RowsShape<MR, C, R>::LV;
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int r0 = gw * rows_per_wave;
+  if (r0 >= p.N) return;
+  const int r1 = min(r0 + rows_per_wave, p.N);
+
+  // ---- this lane's activations: xv[m][c][j] = column c * 1024 + 16 lane + j
+  float xv[MR][C][16];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const bool mok = m < p.M;
+    const uint16_t* xr = p.x + static_cast<int64_t>(mok ? m : 0) * p.xs;
+    if constexpr (MODE == 2) {
+      // s = x (+ residual) in fp32; the RMSNorm kernel's thread t holds the
+      // 8-column chunks t, t + 256, ..., so chunk 128 c + 2 lane + e (e = 0, 1)
+      // is thread 128 (c % 2) + 2 lane + e: lane halves < 32 / >= 32 are its
+      // waves 0 / 1 (even c) and 2 / 3 (odd c), and its xor steps 32 .. 2
+      // are lane xor 16 .. 1 here, step 1 the e pair
+      float ss[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [c % 2][e]
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int k0 = c * 1024 + 16 * lane;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          if (k0 + 8 * e < p.K) {
+            const u32x4 a = sd::load16(xr + k0 + 8 * e);
+            u32x4 bq = {0u, 0u, 0u, 0u};
+            if (p.nres) bq = sd::load16(p.nres + static_cast<int64_t>(m) * p.nres_s + k0 + 8 * e);
+            const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {bq.x, bq.y, bq.z, bq.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              float f = sd::from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
+              if (p.nres) f = f + sd::from_bits<T>(static_cast<uint16_t>(bw[i / 2] >> (16 * (i & 1))));
+              xv[m][c][8 * e + i] = f;
+              ss[c & 1][e] += f * f;
+            }
+            if (p.nres_out && gw == 0 && mok) {
+              uint32_t ro[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) ro[i] = sd::pack2<T>(xv[m][c][8 * e + 2 * i], xv[m][c][8 * e + 2 * i + 1]);
+              sd::store16(p.nres_out + static_cast<int64_t>(m) * p.nres_out_s + k0 + 8 * e,
+                          u32x4{ro[0], ro[1], ro[2], ro[3]});
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[m][c][8 * e + i] = 0.f;
+          }
+        }
+      }
+      float wsum[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int off = 16; off > 0; off >>= 1) ss[h][e] += __shfl_xor(ss[h][e], off);
+        wsum[h] = ss[h][0] + ss[h][1];
+      }
+      float tot = 0.f;
+      tot += __shfl(wsum[0], 0);
+      tot += __shfl(wsum[0], 32);
+      tot += __shfl(wsum[1], 0);
+      tot += __shfl(wsum[1], 32);
+      const float rn = rsqrtf(tot / static_cast<float>(p.K) + p.neps);
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int k0 = c * 1024 + 16 * lane;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          if (k0 + 8 * e < p.K) {
+            const u32x4 wq = sd::load16(p.nw + k0 + 8 * e);
+            const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float n = static_cast<float>(static_cast<T>(xv[m][c][8 * e + i] * rn));
+              const float wv = sd::from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> (16 * (i & 1))));
+              xv[m][c][8 * e + i] = static_cast<float>(static_cast<T>(n * wv));
+            }
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int k0 = c * 1024 + 16 * lane;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          u32x4 a = {0u, 0u, 0u, 0u};
+          if (mok && k0 + 8 * e < p.K) {
+            a = sd::load16(xr + k0 + 8 * e);
+            if constexpr (MODE == 1) a = sd::silu_mul8<T>(a, sd::load16(xr + p.up + k0 + 8 * e));
+          }
+          const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            xv[m][c][8 * e + i] = sd::from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
+        }
+      }
+    }
+  }
+
+  // ---- weight rows, R per batch, two batches in flight
+  auto load = [&](u32x4 (&B)[R][C], int rb) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = min(rb + r, r1 - 1);
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int k0 = min(c * 1024 + 16 * lane, p.K - 16);  // lanes past K: a valid address, unused
+        B[r][c] = sd::load16_stream(p.w + row * p.ws + k0);
+      }
+    }
+  };
+  auto consume = [&](const u32x4 (&B)[R][C], int rb) {
+    float acc[V];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = min(rb + r, r1 - 1);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) acc[r * MR + m] = 0.f;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const uint32_t ww[4] = {B[r][c].x, B[r][c].y, B[r][c].z, B[r][c].w};
+        float part[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) part[m] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float q = static_cast<float>(static_cast<int8_t>(ww[i >> 2] >> (8 * (i & 3))));
+#pragma unroll
+          for (int m = 0; m < MR; ++m) part[m] = fmaf(q, xv[m][c][i], part[m]);
+        }
+        float sc = 1.f;
+        if constexpr (PG) {
+          const int k0 = min(c * 1024 + 16 * lane, p.K - 16);
+          sc = load_scale(p.scale, p.scale_dtype, row * (p.K / p.group) + k0 / p.group);
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[r * MR + m] += PG ? part[m] * sc : part[m];
+      }
+    }
+    // reduce-scatter: after the halving steps lane l holds sum (l >> (6 - LV))
+#pragma unroll
+    for (int h = V / 2, off = 32; h >= 1; h >>= 1, off >>= 1) {
+      const bool upper = lane & off;
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float send = upper ? acc[i] : acc[i + h];
+        const float keep = upper ? acc[i + h] : acc[i];
+        acc[i] = keep + __shfl_xor(send, off);
+      }
+    }
+    float v = acc[0];
+#pragma unroll
+    for (int off = 32 >> LV; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    if ((lane & ((64 >> LV) - 1)) == 0) {
+      const int idx = lane >> (6 - LV);
+      const int r = idx / MR, m = idx - r * MR;
+      const int row = rb + r;
+      if (row < r1 && m < p.M) {
+        if constexpr (!PG) v = v * load_scale(p.scale, p.scale_dtype, row);
+        if (p.bias) v = v + sd::from_bits<T>(p.bias[row]);
+        p.y[static_cast<int64_t>(m) * p.ys + row] = sd::to_bits<T>(v);
+      }
+    }
+  };
+  u32x4 ba[R][C], bb[R][C];
+  load(ba, r0);
+  for (int rb = r0; rb < r1; rb += 2 * R) {
+    load(bb, rb + R < r1 ? rb + R : rb);
+    consume(ba, rb);
+    if (rb + R >= r1) break;
+    load(ba, rb + 2 * R < r1 ? rb + 2 * R : rb);
+    consume(bb, rb + R);
+  }
+}
+
+// Rows per wave and grid of the row-streaming kernel: about 4 rows per wave,
+// at most 8 waves per CU (two per SIMD) over the whole matrix.
+struct RowsPlan {
+  int blocks, rows_per_wave, R;
+};
+
 struct W8Plan {
   int MT, NT, KW, mblocks, groups, grid;
 };
@@ -681,6 +892,68 @@ int launch_all(const W8Params& p, const W8Plan& pl, hipStream_t st) {
   return sd::check_launch("w8a16");
 }
 
+// Row-streaming path: one or two activation rows, K <= 4096 (M * K <= 4096),
+// weights up to 32 MiB (the decoder layers' linears, where launch latency
+// dominates; the tiled kernel streams a large lm_head faster: 29.0 vs 30.7 us
+// at 151936 x 1024); SiLU / norm forms at one row, per-channel scale.
+bool rows_eligible(const W8Params& p, int mode) {
+  const int C = (p.K + 1023) / 1024;
+  if (p.M > 2 || C > 4 || p.M * C > 4) return false;
+  if (static_cast<int64_t>(p.N) * p.K > (int64_t{32} << 20)) return false;
+  return mode == 0 || (p.M == 1 && p.group == 0);
+}
+
+template <typename T, int MR, int C, int MODE, bool PG>
+int launch_rows_c(const W8Params& p, hipStream_t st) {
+  // about 4 rows per wave, at most two waves per SIMD (8 per CU)
+  int64_t waves = static_cast<int64_t>(w8_device_cus()) * 8;
+  const int64_t want = (static_cast<int64_t>(p.N) + 3) / 4;
+  if (want < waves) waves = want;
+  const int blocks = static_cast<int>((waves + kWaves - 1) / kWaves);
+  const int rpw = static_cast<int>((p.N + static_cast<int64_t>(blocks) * kWaves - 1) /
+                                   (static_cast<int64_t>(blocks) * kWaves));
+  if constexpr (MR == 1 && C == 1) {
+    if (rpw >= 32) {
+      hipLaunchKernelGGL((w8a16_rows_kernel<T, 1, 1, 8, MODE, PG>), dim3(blocks), dim3(kThreads),
+                         0, st, p, rpw);
+      return SD_OK;
+    }
+  }
+  hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 4, MODE, PG>), dim3(blocks), dim3(kThreads), 0,
+                     st, p, rpw);
+  return SD_OK;
+}
+
+template <typename T, int MODE, bool PG>
+int launch_rows(const W8Params& p, hipStream_t st) {
+  const int C = (p.K + 1023) / 1024;
+  int rc;
+  if (p.M == 1) {
+    switch (C) {
+      case 1: rc = launch_rows_c<T, 1, 1, MODE, PG>(p, st); break;
+      case 2: rc = launch_rows_c<T, 1, 2, MODE, PG>(p, st); break;
+      case 3: rc = launch_rows_c<T, 1, 3, MODE, PG>(p, st); break;
+      default: rc = launch_rows_c<T, 1, 4, MODE, PG>(p, st); break;
+    }
+  } else {
+    if constexpr (MODE == 0) {
+      rc = C == 1 ? launch_rows_c<T, 2, 1, MODE, PG>(p, st) : launch_rows_c<T, 2, 2, MODE, PG>(p, st);
+    } else {
+      rc = SD_ERR_UNSUPPORTED;  // rows_eligible keeps these on the tiled path
+    }
+  }
+  if (rc != SD_OK) return rc;
+  return sd::check_launch("w8a16 rows");
+}
+
+template <typename T>
+int launch_rows_any(const W8Params& p, int mode, hipStream_t st) {
+  if (mode == 1) return launch_rows<T, 1, false>(p, st);
+  if (mode == 2) return launch_rows<T, 2, false>(p, st);
+  if (p.group) return launch_rows<T, 0, true>(p, st);
+  return launch_rows<T, 0, false>(p, st);
+}
+
 }  // namespace
 
 extern "C" size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_size) {
@@ -775,6 +1048,11 @@ int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& nor
   p.nres_out_s = norm.residual_out_stride;
   p.neps = norm.eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int mode = up >= 0 ? 1 : (p.nw ? 2 : 0);
+  if (rows_eligible(p, mode)) {
+    if (dtype == SD_BF16) return launch_rows_any<__bf16>(p, mode, st);
+    return launch_rows_any<_Float16>(p, mode, st);
+  }
   if (up >= 0) {
     if (dtype == SD_BF16) return launch_all<__bf16, 1>(p, pl, st);
     return launch_all<_Float16, 1>(p, pl, st);

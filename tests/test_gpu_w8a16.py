@@ -185,6 +185,8 @@ def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
 
 
 @pytest.mark.parametrize("M,N,K,gs,act,res", [(1, 4096, 1024, 0, torch.bfloat16, True),
+                                              (1, 2048, 2560, 0, torch.bfloat16, True),
+                                              (1, 512, 4096, 0, torch.float16, False),
                                               (16, 6144, 1024, 0, torch.bfloat16, True),
                                               (40, 1024, 1024, 0, torch.bfloat16, True),
                                               (3, 512, 1152, 0, torch.float16, True),
@@ -255,3 +257,26 @@ def test_rmsnorm_linear_rejects_aliased_residual():
     nw = torch.ones((K,), device=DEV, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="alias"):
         ops.w8a16_rmsnorm_linear(x, nw, 1e-6, c["w"], c["s"], residual=r, residual_out=r)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("K,gs", [(1024, 0), (2560, 0), (2048, 128), (4096, 0), (3072, 64)])
+@pytest.mark.parametrize("act", [torch.bfloat16, torch.float16])
+def test_row_streaming_path(M, K, gs, act):
+    # one or two activation rows at K <= 4096 take the row-streaming kernel
+    # (whole 1 KB weight rows per load, activations in registers): per channel
+    # and per group, bias, a partial last 1024-column chunk (K = 2560), and
+    # N not a multiple of the rows per wave
+    if M * ((K + 1023) // 1024) > 4:
+        pytest.skip("M * ceil(K / 1024) > 4 takes the tiled kernel")
+    N = 3001
+    c = workloads.w8a16_case(M, N, K, seed=K + M, act_dtype=act)
+    g = workloads.device_generator(DEV, K + 7)
+    if gs:
+        s = (torch.rand((N, K // gs), generator=g, device=DEV) * 3e-3 + 1e-3).to(act)
+    else:
+        s = c["s"]
+    bias = torch.randn((N,), generator=g, device=DEV).to(act)
+    y = ops.w8a16_linear(c["x"], c["w"], s, bias, group_size=gs)
+    check(y, c["x"], c["w"], s, bias, "per_group" if gs else "per_channel", gs,
+          out_rel=2.0 ** -9 if act == torch.float16 else 2.0 ** -8, what=f"rows M={M} K={K} gs={gs}")
