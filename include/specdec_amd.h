@@ -192,10 +192,11 @@ size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_si
  *   bias  : (N,) dtype or NULL
  *   y     : (M, N) dtype, row stride y_stride_m
  * Dequantization is fused (int8 -> fp in registers, fp32 accumulation, scale
- * applied to the fp32 accumulator). M <= 2 on weights up to 32 MiB (K <= 4096,
- * M * ceil(K / 1024) <= 4) streams whole weight rows through fp32 FMAs; other
- * shapes run the MFMA kernel. Supported: K % 64 == 0, group_size 0 or a
- * multiple of 64 dividing K. `workspace` may be NULL.
+ * applied to the fp32 accumulator). One or two activation rows with a
+ * per-channel scale on weights up to 32 MiB (M * ceil(K / 1024) <= 4) stream
+ * whole weight rows through fp32 FMAs; other shapes run the MFMA kernel (the
+ * SiLU and RMSNorm forms below follow the same rule). Supported: K % 64 == 0,
+ * group_size 0 or a multiple of 64 dividing K. `workspace` may be NULL.
  */
 int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t w_stride_n,
                     const void* scale, int32_t scale_dtype, int32_t group_size,

@@ -488,10 +488,9 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 // forms bit for bit. Products accumulate in fp32 per lane (one conversion and
 // one FMA per weight), then the R x MR sums of a batch reduce across the
 // lanes in one reduce-scatter (halving steps, then plain xor steps), so a
-// row's result is always summed in the same order. No MFMA, no LDS: at one or
-// two rows the MFMA form spends its time on operand staging, not on math.
-// Per group (PG): lane l's 16 columns of chunk c lie in one group; its partial
-// is scaled before the reduction.
+// row's result is always summed in the same order. No MFMA, no LDS: at a few
+// rows the MFMA form spends its time on operand staging, not on math.
+// Per-channel scales only (applied to the reduced sum).
 template <int MR, int C, int R>
 struct RowsShape {
   static constexpr int V = R * MR;  // sums per lane per batch
@@ -499,7 +498,7 @@ struct RowsShape {
   static_assert((1 << LV) == V, "R * MR must be a power of two <= 16");
 };
 
-template <typename T, int MR, int C, int R, int MODE, bool PG>
+template <typename T, int MR, int C, int R, int MODE>
 __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int rows_per_wave) {
 #pragma clang fp contract(off)
   constexpr int V = RowsShape<MR, C, R>::V, LV = RowsShape<MR, C, R>::LV;
@@ -635,13 +634,8 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
 #pragma unroll
           for (int m = 0; m < MR; ++m) part[m] = fmaf(q, xv[m][c][i], part[m]);
         }
-        float sc = 1.f;
-        if constexpr (PG) {
-          const int k0 = min(c * 1024 + 16 * lane, p.K - 16);
-          sc = load_scale(p.scale, p.scale_dtype, row * (p.K / p.group) + k0 / p.group);
-        }
 #pragma unroll
-        for (int m = 0; m < MR; ++m) acc[r * MR + m] += PG ? part[m] * sc : part[m];
+        for (int m = 0; m < MR; ++m) acc[r * MR + m] += part[m];
       }
     }
     // reduce-scatter: after the halving steps lane l holds sum (l >> (6 - LV))
@@ -663,7 +657,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
       const int r = idx / MR, m = idx - r * MR;
       const int row = rb + r;
       if (row < r1 && m < p.M) {
-        if constexpr (!PG) v = v * load_scale(p.scale, p.scale_dtype, row);
+        v = v * load_scale(p.scale, p.scale_dtype, row);
         if (p.bias) v = v + sd::from_bits<T>(p.bias[row]);
         p.y[static_cast<int64_t>(m) * p.ys + row] = sd::to_bits<T>(v);
       }
@@ -892,18 +886,22 @@ int launch_all(const W8Params& p, const W8Plan& pl, hipStream_t st) {
   return sd::check_launch("w8a16");
 }
 
-// Row-streaming path: one or two activation rows, K <= 4096 (M * K <= 4096),
+// Row-streaming path: one or two activation rows with M * ceil(K / 1024) <= 4,
 // weights up to 32 MiB (the decoder layers' linears, where launch latency
 // dominates; the tiled kernel streams a large lm_head faster: 29.0 vs 30.7 us
-// at 151936 x 1024); SiLU / norm forms at one row, per-channel scale.
+// at 151936 x 1024, and is faster from 4 rows up: qkv at M = 7 4.6 vs 4.9 us
+// with 8 rows here), per-channel scale. The rule is the same for the plain,
+// SiLU and norm forms, so a fused call and its two-launch form always run the
+// same GEMV.
 bool rows_eligible(const W8Params& p, int mode) {
   const int C = (p.K + 1023) / 1024;
-  if (p.M > 2 || C > 4 || p.M * C > 4) return false;
+  if (p.M > 2 || p.M * C > 4) return false;
   if (static_cast<int64_t>(p.N) * p.K > (int64_t{32} << 20)) return false;
-  return mode == 0 || (p.M == 1 && p.group == 0);
+  (void)mode;
+  return p.group == 0;
 }
 
-template <typename T, int MR, int C, int MODE, bool PG>
+template <typename T, int MR, int C, int MODE>
 int launch_rows_c(const W8Params& p, hipStream_t st) {
   // about 4 rows per wave, at most two waves per SIMD (8 per CU)
   int64_t waves = static_cast<int64_t>(w8_device_cus()) * 8;
@@ -914,33 +912,29 @@ int launch_rows_c(const W8Params& p, hipStream_t st) {
                                    (static_cast<int64_t>(blocks) * kWaves));
   if constexpr (MR == 1 && C == 1) {
     if (rpw >= 32) {
-      hipLaunchKernelGGL((w8a16_rows_kernel<T, 1, 1, 8, MODE, PG>), dim3(blocks), dim3(kThreads),
+      hipLaunchKernelGGL((w8a16_rows_kernel<T, 1, 1, 8, MODE>), dim3(blocks), dim3(kThreads),
                          0, st, p, rpw);
       return SD_OK;
     }
   }
-  hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 4, MODE, PG>), dim3(blocks), dim3(kThreads), 0,
+  hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 4, MODE>), dim3(blocks), dim3(kThreads), 0,
                      st, p, rpw);
   return SD_OK;
 }
 
-template <typename T, int MODE, bool PG>
+template <typename T, int MODE>
 int launch_rows(const W8Params& p, hipStream_t st) {
   const int C = (p.K + 1023) / 1024;
   int rc;
   if (p.M == 1) {
     switch (C) {
-      case 1: rc = launch_rows_c<T, 1, 1, MODE, PG>(p, st); break;
-      case 2: rc = launch_rows_c<T, 1, 2, MODE, PG>(p, st); break;
-      case 3: rc = launch_rows_c<T, 1, 3, MODE, PG>(p, st); break;
-      default: rc = launch_rows_c<T, 1, 4, MODE, PG>(p, st); break;
+      case 1: rc = launch_rows_c<T, 1, 1, MODE>(p, st); break;
+      case 2: rc = launch_rows_c<T, 1, 2, MODE>(p, st); break;
+      case 3: rc = launch_rows_c<T, 1, 3, MODE>(p, st); break;
+      default: rc = launch_rows_c<T, 1, 4, MODE>(p, st); break;
     }
   } else {
-    if constexpr (MODE == 0) {
-      rc = C == 1 ? launch_rows_c<T, 2, 1, MODE, PG>(p, st) : launch_rows_c<T, 2, 2, MODE, PG>(p, st);
-    } else {
-      rc = SD_ERR_UNSUPPORTED;  // rows_eligible keeps these on the tiled path
-    }
+    rc = C == 1 ? launch_rows_c<T, 2, 1, MODE>(p, st) : launch_rows_c<T, 2, 2, MODE>(p, st);
   }
   if (rc != SD_OK) return rc;
   return sd::check_launch("w8a16 rows");
@@ -948,10 +942,9 @@ int launch_rows(const W8Params& p, hipStream_t st) {
 
 template <typename T>
 int launch_rows_any(const W8Params& p, int mode, hipStream_t st) {
-  if (mode == 1) return launch_rows<T, 1, false>(p, st);
-  if (mode == 2) return launch_rows<T, 2, false>(p, st);
-  if (p.group) return launch_rows<T, 0, true>(p, st);
-  return launch_rows<T, 0, false>(p, st);
+  if (mode == 1) return launch_rows<T, 1>(p, st);
+  if (mode == 2) return launch_rows<T, 2>(p, st);
+  return launch_rows<T, 0>(p, st);
 }
 
 }  // namespace

@@ -158,6 +158,7 @@ def test_errors():
 
 
 @pytest.mark.parametrize("M,N,K,gs,act", [(1, 1024, 3072, 0, torch.bfloat16),
+                                          (2, 1024, 1024, 0, torch.bfloat16),
                                           (7, 1024, 3072, 0, torch.float16),
                                           (56, 1024, 3072, 0, torch.bfloat16),
                                           (3, 33000, 1024, 0, torch.bfloat16),
@@ -186,6 +187,7 @@ def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
 
 @pytest.mark.parametrize("M,N,K,gs,act,res", [(1, 4096, 1024, 0, torch.bfloat16, True),
                                               (1, 2048, 2560, 0, torch.bfloat16, True),
+                                              (2, 2048, 1024, 0, torch.float16, True),
                                               (1, 512, 4096, 0, torch.float16, False),
                                               (16, 6144, 1024, 0, torch.bfloat16, True),
                                               (40, 1024, 1024, 0, torch.bfloat16, True),
@@ -263,12 +265,13 @@ def test_rmsnorm_linear_rejects_aliased_residual():
 @pytest.mark.parametrize("K,gs", [(1024, 0), (2560, 0), (2048, 128), (4096, 0), (3072, 64)])
 @pytest.mark.parametrize("act", [torch.bfloat16, torch.float16])
 def test_row_streaming_path(M, K, gs, act):
-    # one or two activation rows at K <= 4096 take the row-streaming kernel
-    # (whole 1 KB weight rows per load, activations in registers): per channel
-    # and per group, bias, a partial last 1024-column chunk (K = 2560), and
-    # N not a multiple of the rows per wave
+    # one or two activation rows at small K with a per-channel scale take the
+    # row-streaming kernel (whole 1 KB weight rows per load, activations in
+    # registers): bias, a partial last 1024-column chunk (K = 2560), N not a
+    # multiple of the rows per wave; the per-group cases check the tiled kernel
+    # at the same shapes
     if M * ((K + 1023) // 1024) > 4:
-        pytest.skip("M * ceil(K / 1024) > 4 takes the tiled kernel")
+        pytest.skip("this M x K takes the tiled kernel")
     N = 3001
     c = workloads.w8a16_case(M, N, K, seed=K + M, act_dtype=act)
     g = workloads.device_generator(DEV, K + 7)
