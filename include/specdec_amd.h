@@ -212,11 +212,13 @@ int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t 
  * the fusion saves the SiluAndMul launch and its round trip through memory.
  * The activation equals sd_silu_mul's output bit for bit, so y equals
  * sd_silu_mul followed by sd_w8a16_linear. gate_up: (M, >= 2K) dtype, row
- * stride gate_up_stride_m; the rest as sd_w8a16_linear (no workspace). The
- * SiLU is computed once per workgroup while its activation rows are staged in
- * LDS, which holds while min(M, 16) * (2 K + 16) <= 33,024 bytes (M = 1 for
- * K = 3072); beyond that the result is the same but each wave recomputes the
- * SiLU of its operands, slower than the two separate calls.
+ * stride gate_up_stride_m; the rest as sd_w8a16_linear (no workspace). On the
+ * row-streaming path (one or two rows, see sd_w8a16_linear) each wave forms
+ * the SiLU of its columns once; otherwise it is computed once per workgroup
+ * while its activation rows are staged in LDS, which holds while
+ * min(M, 16) * (2 K + 16) <= 33,024 bytes; beyond that the result is the same
+ * but each wave recomputes the SiLU of its operands, slower than the two
+ * separate calls.
  */
 int sd_w8a16_silu_linear(const void* gate_up, int64_t gate_up_stride_m, const int8_t* w,
                          int64_t w_stride_n, const void* scale, int32_t scale_dtype,
@@ -233,12 +235,13 @@ int sd_w8a16_silu_linear(const void* gate_up, int64_t gate_up_stride_m, const in
  * so y equals sd_rmsnorm followed by sd_w8a16_linear; with a residual,
  * residual_out (may be NULL) receives bf16(x + residual) as sd_rmsnorm's
  * residual_out does, written by one workgroup per row block. residual_out may
- * alias neither x nor residual (other workgroups still read them). Each
- * workgroup normalises its activation rows, one after another, while staging
- * them in LDS: the form pays for a few rows (decode: about 1.4 us saved at
- * M = 1 on MI355X, break-even near M = 5), not for many. A block that does not
- * fit (min(M, 16) (2 K + 16) > 33,024 bytes is never promised) returns
- * SD_ERR_UNSUPPORTED and the caller runs the two calls.
+ * alias neither x nor residual (other workgroups still read them). On the
+ * row-streaming path (one or two rows, see sd_w8a16_linear) every wave forms
+ * the norm of its columns; otherwise each workgroup normalises its activation
+ * rows, one after another, while staging them in LDS. The form pays for a few
+ * rows (decode), not for many (break-even near M = 5 on MI355X). A block that
+ * does not fit the staging LDS (min(M, 16) (2 K + 16) > 33,024 bytes is never
+ * promised) returns SD_ERR_UNSUPPORTED and the caller runs the two calls.
  *   x, residual, residual_out: (M, K) dtype, 16-byte aligned rows;
  *   norm_weight: (K,) dtype; K % 8 == 0, K <= 8192; the rest as
  *   sd_w8a16_linear (no workspace).

@@ -318,9 +318,11 @@ def w8a16_rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     The normalised rows equal ``rmsnorm``'s bit for bit. With ``residual``,
     ``residual_out`` (aliasing neither x nor residual; None: not written)
     receives bf16(x + residual), ``rmsnorm``'s second output. One launch for
-    up to 4 rows (every workgroup normalises its rows one after another: about
-    1.4 us saved at one row, break-even near five), the two separate launches
-    for more rows or when the rows do not fit the staging LDS (same results)."""
+    up to 4 rows: at one or two rows every wave of the row-streaming GEMV
+    forms the norm of its columns; at three or four the tiled kernel's
+    workgroups normalise their rows while staging them (break-even near five
+    rows). More rows, or rows that do not fit the staging LDS, take the two
+    separate launches (same results)."""
     assert qweight.dtype == torch.int8 and qweight.dim() == 2
     N, K = qweight.shape
     assert x.shape[-1] == K and norm_weight.shape == (K,)
