@@ -98,9 +98,11 @@ class DraftChain:
         p = torch.arange(k, dtype=torch.int64)[:, None] + ctx_len  # (k, 1)
         pos_k = p.expand(k, batch)
         blk = bt.gather(1, (pos_k // block_size).T.contiguous()).T  # (k, B)
-        self.positions = pos_k.to(self.dev)
-        self.slots = (blk.to(torch.int64) * block_size + pos_k % block_size).to(torch.int32).to(self.dev)
-        self.ctx = (pos_k + 1).to(torch.int32).to(self.dev)
+        # row-contiguous (k, B): each step's row is handed to the kernels as is
+        self.positions = pos_k.contiguous().to(self.dev)
+        self.slots = (blk.to(torch.int64) * block_size + pos_k % block_size).to(torch.int32) \
+            .contiguous().to(self.dev)
+        self.ctx = (pos_k + 1).to(torch.int32).contiguous().to(self.dev)
 
         # static token buffers: tokens[0] = the last context token, tokens[s+1] = step s output
         self.tokens = torch.randint(0, vocab, (k + 1, batch), generator=cg).to(self.dev)
