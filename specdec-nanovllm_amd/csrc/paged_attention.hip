@@ -15,7 +15,9 @@
 //   S = max(ceil(C / R), min_steps) columns. A workgroup has NW wave64s (NW
 //   divides Hkv: 4, 2 or 1) and takes heads hg NW .. hg NW + NW - 1 of one run
 //   (workgroup w: run w / (Hkv / NW), head group w % (Hkv / NW)): wave i owns
-//   head hg NW + i, and all NW waves walk the same columns, so the workgroup
+//   head hg NW + i, and all NW waves walk the same columns (with two row tiles,
+//   verify: two waves per head take the two halves of 64-key columns and
+//   merge in LDS at the flush, KS = 2), so the workgroup
 //   reads NW adjacent 256-byte head rows (NW x 256 contiguous bytes) of every
 //   key instead of one. Every workgroup streams the same number of bytes
 //   whatever the length mix, with no host sync: each workgroup derives C and
@@ -57,7 +59,7 @@ using sd::u32x4;
 
 constexpr int kD = 128;                // head_dim
 constexpr int kThreads = 256;          // combine kernel
-constexpr int kStep = 32;              // keys of a column: one workgroup step
+constexpr int kStep = 32;              // keys of one wave's share of a column
 constexpr int kKPitch = 136;  // 16-bit elements per LDS row of a K tile (272 B: b128 reads of
                               // 16 consecutive rows hit distinct banks)
 constexpr int kVPitch = 144;  // same for a V tile (288 B: transpose reads of 4 x 4 rows hit
@@ -92,6 +94,7 @@ struct AttnParams {
   int32_t nwg;        // workgroups: runs * (Hkv / NW)
   int32_t runs;
   int32_t min_steps;  // lower bound of columns per run
+  int32_t col_keys;   // keys per column: 32 KS (KS waves per kv head)
   int32_t comb_rows;  // query rows per combine workgroup (a power of two <= 8)
   int32_t rmax;       // G * max_qlen
   // Fused store_kvcache (knew == NULL: none). Query row t's key/value row is
@@ -142,7 +145,9 @@ __device__ __forceinline__ int walk_keys_uniform(const AttnParams& p, int b) {
   return L;
 }
 
-__device__ __forceinline__ int steps_of(int L) { return (L + kStep - 1) / kStep; }
+__device__ __forceinline__ int steps_of(const AttnParams& p, int L) {
+  return (L + p.col_keys - 1) / p.col_keys;
+}
 
 template <bool STORE>
 __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b) {
@@ -168,7 +173,7 @@ __device__ int cols_before(const AttnParams& p, int upto) {
   int sum = 0;
   for (int c = 0; c < upto; c += 64) {
     const int b = c + lane;
-    sum += b < upto ? steps_of(walk_keys<STORE>(p, b)) : 0;
+    sum += b < upto ? steps_of(p, walk_keys<STORE>(p, b)) : 0;
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
@@ -183,7 +188,7 @@ __device__ void locate(const AttnParams& p, int s, int& b_out, int& first_out) {
   int run = 0;
   for (int c = 0; c < p.num_seqs; c += 64) {
     const int b = c + lane;
-    const int n = b < p.num_seqs ? steps_of(walk_keys<STORE>(p, b)) : 0;
+    const int n = b < p.num_seqs ? steps_of(p, walk_keys<STORE>(p, b)) : 0;
     int incl = n;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -290,7 +295,10 @@ struct StepRegs {
 template <int RT>
 constexpr int main_occupancy() { return RT == 1 ? 2 : 1; }
 
-template <typename T, int RT, bool ONE_PAGE, bool STORE, int NW>
+// KS = 2: two waves per kv head take the two 32-key halves of a 64-key column
+// and merge their states in LDS when a pair ends, so a run covers twice the
+// keys and the pairs leave half the partials (verify's two row tiles).
+template <typename T, int RT, bool ONE_PAGE, bool STORE, int NW, int KS = 1>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(main_occupancy<RT>())))
 void paged_attn_main(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[smem_bytes<NW>()];
@@ -301,8 +309,10 @@ void paged_attn_main(AttnParams p) {
   const int lr = lane & 15, lg = lane >> 4;
 
   // ---- this wave's kv head and the workgroup's run of columns [s0, s1)
-  const int groups = p.Hkv / NW;
-  const int h = static_cast<int>(blockIdx.x) % groups * NW + wave;
+  constexpr int HPW = NW / KS;  // kv heads per workgroup
+  const int groups = p.Hkv / HPW;
+  const int h = static_cast<int>(blockIdx.x) % groups * HPW + wave / KS;
+  const int ks = wave % KS;  // this wave's 32-key half of a column (KS = 2)
   const int run = static_cast<int>(blockIdx.x) / groups;
   const int total = __builtin_amdgcn_readfirstlane(cols_before<STORE>(p, p.num_seqs));
   const int S = max((total + p.runs - 1) / p.runs, p.min_steps);
@@ -315,7 +325,7 @@ void paged_attn_main(AttnParams p) {
   first = __builtin_amdgcn_readfirstlane(first);
 
   SeqInfo si = seq_info<STORE>(p, b);
-  int n = steps_of(si.L);  // columns of sequence b
+  int n = steps_of(p, si.L);  // columns of sequence b
   int j = s0 - first;
   int j_first = j;  // column at which this workgroup entered the current pair
 
@@ -356,11 +366,11 @@ void paged_attn_main(AttnParams p) {
     // wave-uniform by construction; readfirstlane lets the compiler prove it, so
     // the block-table lookup is a scalar load (lgkmcnt) and never waits on the
     // vector loads in flight
-    const int t0 = __builtin_amdgcn_readfirstlane(min(lj * kStep, last));
+    const int t0 = __builtin_amdgcn_readfirstlane(min(lj * p.col_keys + ks * kStep, last));
     lb = __builtin_amdgcn_readfirstlane(lb);
     const int32_t* btrow = p.bt + static_cast<int64_t>(lb) * p.bt_stride;
     const int64_t hoff = static_cast<int64_t>(lh) * p.c_shead;
-    const bool used = real && lj * kStep <= last;  // workgroup-uniform
+    const bool used = real && lj * p.col_keys + ks * kStep <= last;  // wave-uniform
     if constexpr (ONE_PAGE) {
       // scalar page base + 32-bit lane offsets (key rows of one page)
       const int64_t base = kv_row<true>(p, btrow, t0) + hoff;
@@ -389,8 +399,8 @@ void paged_attn_main(AttnParams p) {
   uint16_t* vl = kl + kStep * kKPitch;
 
   auto compute_step = [&](StepRegs& R, int cj) {
-    const int tb = cj * kStep;
-    if (tb >= si.L) return;  // workgroup-uniform
+    const int tb = cj * p.col_keys + ks * kStep;
+    if (tb >= si.L) return;  // wave-uniform (KS = 2: the last half of a column may be empty)
     // ---- stage the 32 K and V rows of this step (row-major, padded pitch)
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -491,9 +501,49 @@ void paged_attn_main(AttnParams p) {
   // row 16 rt + lr, dims 16 dt + 4 lg .. +4 of tile rt.
   auto flush = [&](bool complete) {
     const int64_t wslot = (static_cast<int64_t>(run) + b) * p.Hkv + h;
+    float lsum[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) lsum[rt] = sd::sum_over_groups(l_run[rt]);
+    if constexpr (KS == 2) {
+      // the second wave of a head hands (m, l, acc) to the first through its
+      // own (idle) K/V tile: rows of kD + 4 floats
+      constexpr int kPitch = kD + 4;
+      static_assert(RT * 16 * kPitch * 4 <= kStep * (kKPitch + kVPitch) * 2, "state fits the tile");
+      __syncthreads();  // every wave is done with its tiles
+      if (ks == 1) {
+        float* xs = reinterpret_cast<float*>(kl);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          float* xr = xs + (rt * 16 + lr) * kPitch;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt)
+            sd::store16(xr + dt * 16 + lg * 4, __builtin_bit_cast(u32x4, acc[rt][dt]));
+          if (lg == 0) *reinterpret_cast<float2*>(xr + kD) = make_float2(m_run[rt], lsum[rt]);
+        }
+      }
+      __syncthreads();
+      if (ks == 0) {
+        const float* ys = reinterpret_cast<const float*>(kl + kStep * (kKPitch + kVPitch));
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const float* yr = ys + (rt * 16 + lr) * kPitch;
+          const float2 ml = *reinterpret_cast<const float2*>(yr + kD);
+          const float M = fmaxf(m_run[rt], ml.x);
+          const float a = m_run[rt] == -INFINITY ? 0.f : exp2f(m_run[rt] - M);
+          const float c = ml.x == -INFINITY ? 0.f : exp2f(ml.x - M);
+          lsum[rt] = lsum[rt] * a + ml.y * c;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt)
+            acc[rt][dt] = acc[rt][dt] * a +
+                          c * __builtin_bit_cast(f32x4, sd::load16(yr + dt * 16 + lg * 4));
+          m_run[rt] = M;
+        }
+      }
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const float l = sd::sum_over_groups(l_run[rt]);
+      if (KS == 2 && ks != 0) break;
+      const float l = lsum[rt];
       const int row = rt * 16 + lr;
       const int qi = row / p.G, g = row - qi * p.G;
       const int64_t qt = si.q0 + qi;
@@ -511,6 +561,7 @@ void paged_attn_main(AttnParams p) {
         if (lg == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * e) = make_float2(m_run[rt], l);
       }
     }
+    if constexpr (KS == 2) __syncthreads();  // the tile is read before the next step stages into it
   };
 
   // ---- walk [s0, s1): load step s + 1 while computing step s
@@ -541,7 +592,7 @@ void paged_attn_main(AttnParams p) {
     if (nb != b) {
       b = nb;
       si = seq_info<STORE>(p, b);
-      n = steps_of(si.L);
+      n = steps_of(p, si.L);
       j_first = 0;
       begin_pair();
     }
@@ -570,7 +621,7 @@ __device__ void cols_split(const AttnParams& p, int b, int& before, int& total) 
   int sb = 0, st = 0;
   for (int c = 0; c < p.num_seqs; c += 64) {
     const int s = c + lane;
-    const int n = s < p.num_seqs ? steps_of(walk_keys<STORE>(p, s)) : 0;
+    const int n = s < p.num_seqs ? steps_of(p, walk_keys<STORE>(p, s)) : 0;
     st += n;
     sb += s < b ? n : 0;
   }
@@ -614,7 +665,7 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   const int qi = row / p.G, g = row - qi * p.G;
   const int64_t qt = si.q0 + qi;
   const bool live = row < si.R && qt >= 0 && qt < p.total_q;
-  const int n = steps_of(si.L);
+  const int n = steps_of(p, si.L);
 
   // STORE: the new rows' key / value / slot and this row's q, loaded now
   f32x4 qv = {0.f, 0.f, 0.f, 0.f}, kn[kNewMax], vn[kNewMax];
@@ -775,7 +826,8 @@ __global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
 // ------------------------------------------------------------------ host
 struct Plan {
   int RT;         // 16-row tiles of query rows
-  int NW;         // waves (= kv heads) per main workgroup
+  int KS;         // waves per kv head (two 32-key halves of a column when 2)
+  int NW;         // waves per main workgroup
   int runs;
   int nwg;        // workgroups of the main grid: runs * Hkv / NW
   int min_steps;  // lower bound of columns per run
@@ -807,17 +859,19 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   const int G = Hq / Hkv;
   pl.rmax = G * max_qlen;
   pl.RT = pl.rmax <= 16 ? 1 : 2;
-  pl.NW = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
+  // two row tiles (verify): two waves per kv head, half the runs and partials
+  pl.KS = pl.RT == 2 && Hkv % 2 == 0 ? 2 : 1;
+  pl.NW = pl.KS == 2 ? 4 : (Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1));
   int64_t runs;
   if (num_splits > 0) {
     runs = static_cast<int64_t>(num_splits) * num_seqs;
     pl.min_steps = 1;
   } else {
     const int occ = pl.RT == 1 ? main_occupancy<1>() : main_occupancy<2>();
-    runs = static_cast<int64_t>(device_cus()) * 4 * occ / Hkv;
-    pl.min_steps = pl.RT == 1 ? 1 : 2;
+    runs = static_cast<int64_t>(device_cus()) * 4 * occ / (Hkv * pl.KS);
+    pl.min_steps = pl.RT == 1 || pl.KS == 2 ? 1 : 2;  // at least 64 keys per run with two tiles
   }
-  const int groups = Hkv / pl.NW;
+  const int groups = Hkv / (pl.NW / pl.KS);
   const int64_t cap = (1 << 20) / groups > 1 ? (1 << 20) / groups : 1;  // grid of at most 2^20
   runs = runs < 1 ? 1 : (runs > cap ? cap : runs);
   pl.runs = static_cast<int>(runs);
@@ -834,33 +888,36 @@ size_t ws_bytes(const Plan& pl) {
   return ml_bytes(pl) + static_cast<size_t>(pl.slots) * pl.rmax * kD * sizeof(float);
 }
 
-template <typename T, int RT, bool STORE, int NW>
+template <typename T, int RT, bool STORE, int NW, int KS = 1>
 void launch_main(const AttnParams& p, hipStream_t st) {
   if (p.block_size % kStep == 0)
-    hipLaunchKernelGGL((paged_attn_main<T, RT, true, STORE, NW>), dim3(p.nwg), dim3(NW * 64), 0,
-                       st, p);
+    hipLaunchKernelGGL((paged_attn_main<T, RT, true, STORE, NW, KS>), dim3(p.nwg), dim3(NW * 64),
+                       0, st, p);
   else
-    hipLaunchKernelGGL((paged_attn_main<T, RT, false, STORE, NW>), dim3(p.nwg), dim3(NW * 64), 0,
-                       st, p);
+    hipLaunchKernelGGL((paged_attn_main<T, RT, false, STORE, NW, KS>), dim3(p.nwg),
+                       dim3(NW * 64), 0, st, p);
 }
 
 template <typename T, int RT, bool STORE>
-void launch_main(const AttnParams& p, int NW, hipStream_t st) {
-  if (NW == 4) launch_main<T, RT, STORE, 4>(p, st);
-  else if (NW == 2) launch_main<T, RT, STORE, 2>(p, st);
+void launch_main(const AttnParams& p, const Plan& pl, hipStream_t st) {
+  if constexpr (RT == 2) {
+    if (pl.KS == 2) return launch_main<T, 2, STORE, 4, 2>(p, st);
+  }
+  if (pl.NW == 4) launch_main<T, RT, STORE, 4>(p, st);
+  else if (pl.NW == 2) launch_main<T, RT, STORE, 2>(p, st);
   else launch_main<T, RT, STORE, 1>(p, st);
 }
 
 template <typename T, int RT>
-void launch_main(const AttnParams& p, int NW, hipStream_t st) {
-  if (p.knew) launch_main<T, RT, true>(p, NW, st);
-  else launch_main<T, RT, false>(p, NW, st);
+void launch_main(const AttnParams& p, const Plan& pl, hipStream_t st) {
+  if (p.knew) launch_main<T, RT, true>(p, pl, st);
+  else launch_main<T, RT, false>(p, pl, st);
 }
 
 template <typename T>
 int launch_all(const AttnParams& p, const Plan& pl, bool combine, hipStream_t st) {
-  if (pl.RT == 1) launch_main<T, 1>(p, pl.NW, st);
-  else launch_main<T, 2>(p, pl.NW, st);
+  if (pl.RT == 1) launch_main<T, 1>(p, pl, st);
+  else launch_main<T, 2>(p, pl, st);
   int rc = sd::check_launch("paged_attention main");
   if (rc != SD_OK || !combine) return rc;
   const dim3 grid((pl.rmax + p.comb_rows - 1) / p.comb_rows, p.Hkv, p.num_seqs);
@@ -998,6 +1055,7 @@ int run_attention(bool combine, const NewRows& nr, const void* q, int64_t q_stri
   p.nwg = pl.nwg;
   p.runs = pl.runs;
   p.min_steps = pl.min_steps;
+  p.col_keys = kStep * pl.KS;
   // rows per combine workgroup: few rows (decode) leave groups free to split
   // each row's partials
   p.comb_rows = 1;
