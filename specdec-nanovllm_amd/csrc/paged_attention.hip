@@ -15,9 +15,9 @@
 //   S = max(ceil(C / R), min_steps) columns. A workgroup has NW wave64s (NW
 //   divides Hkv: 4, 2 or 1) and takes heads hg NW .. hg NW + NW - 1 of one run
 //   (workgroup w: run w / (Hkv / NW), head group w % (Hkv / NW)): wave i owns
-//   head hg NW + i, and all NW waves walk the same columns (with two row tiles,
-//   verify: two waves per head take the two halves of 64-key columns and
-//   merge in LDS at the flush, KS = 2), so the workgroup
+//   head hg NW + i, and all NW waves walk the same columns (two row tiles, or
+//   at most 4 sequences: two waves per head take the two halves of 64-key
+//   columns and merge in LDS at the flush, KS = 2), so the workgroup
 //   reads NW adjacent 256-byte head rows (NW x 256 contiguous bytes) of every
 //   key instead of one. Every workgroup streams the same number of bytes
 //   whatever the length mix, with no host sync: each workgroup derives C and
@@ -297,7 +297,8 @@ constexpr int main_occupancy() { return RT == 1 ? 2 : 1; }
 
 // KS = 2: two waves per kv head take the two 32-key halves of a 64-key column
 // and merge their states in LDS when a pair ends, so a run covers twice the
-// keys and the pairs leave half the partials (verify's two row tiles).
+// keys and the pairs leave half the partials (verify's two row tiles, small
+// batches).
 template <typename T, int RT, bool ONE_PAGE, bool STORE, int NW, int KS = 1>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(main_occupancy<RT>())))
 void paged_attn_main(AttnParams p) {
@@ -859,8 +860,9 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   const int G = Hq / Hkv;
   pl.rmax = G * max_qlen;
   pl.RT = pl.rmax <= 16 ? 1 : 2;
-  // two row tiles (verify): two waves per kv head, half the runs and partials
-  pl.KS = pl.RT == 2 && Hkv % 2 == 0 ? 2 : 1;
+  // two waves per kv head, half the runs and partials: two row tiles (verify),
+  // and small batches, whose pairs each collect a partial from many runs
+  pl.KS = (pl.RT == 2 || num_seqs <= 4) && Hkv % 2 == 0 ? 2 : 1;
   pl.NW = pl.KS == 2 ? 4 : (Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1));
   int64_t runs;
   if (num_splits > 0) {
@@ -900,9 +902,7 @@ void launch_main(const AttnParams& p, hipStream_t st) {
 
 template <typename T, int RT, bool STORE>
 void launch_main(const AttnParams& p, const Plan& pl, hipStream_t st) {
-  if constexpr (RT == 2) {
-    if (pl.KS == 2) return launch_main<T, 2, STORE, 4, 2>(p, st);
-  }
+  if (pl.KS == 2) return launch_main<T, RT, STORE, 4, 2>(p, st);
   if (pl.NW == 4) launch_main<T, RT, STORE, 4>(p, st);
   else if (pl.NW == 2) launch_main<T, RT, STORE, 2>(p, st);
   else launch_main<T, RT, STORE, 1>(p, st);
