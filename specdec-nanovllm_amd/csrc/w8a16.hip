@@ -893,11 +893,10 @@ int launch_all(const W8Params& p, const W8Plan& pl, hipStream_t st) {
 // with 8 rows here), per-channel scale. The rule is the same for the plain,
 // SiLU and norm forms, so a fused call and its two-launch form always run the
 // same GEMV.
-bool rows_eligible(const W8Params& p, int mode) {
+bool rows_eligible(const W8Params& p) {
   const int C = (p.K + 1023) / 1024;
   if (p.M > 2 || p.M * C > 4) return false;
   if (static_cast<int64_t>(p.N) * p.K > (int64_t{32} << 20)) return false;
-  (void)mode;
   return p.group == 0;
 }
 
@@ -1042,7 +1041,7 @@ int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& nor
   p.neps = norm.eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int mode = up >= 0 ? 1 : (p.nw ? 2 : 0);
-  if (rows_eligible(p, mode)) {
+  if (rows_eligible(p)) {
     if (dtype == SD_BF16) return launch_rows_any<__bf16>(p, mode, st);
     return launch_rows_any<_Float16>(p, mode, st);
   }
