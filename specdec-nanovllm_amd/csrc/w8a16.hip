@@ -123,6 +123,12 @@ template <> __device__ __forceinline__ u32x4 dequant8<__bf16>(uint32_t w0, uint3
 // (SWZ = min(4 U, 16) - 1), from which each lane reads its MFMA A operand
 // (16 int8 of row l % 16 at k = 64 step + 16 (l / 16)) with ds_read_b128; with
 // 16 positions per row the 16 lanes of a read hit distinct banks.
+// The exception is the staged form with 32 activation rows (XL, MT = 2): there
+// each lane loads its A operand directly (a load instruction then covers 16
+// rows x 64 bytes, half cache lines, which costs the narrower shapes 2-20%),
+// because without the weight tile two workgroups fit per CU beside the
+// 64 KB of activation rows, and the MFMA work per weight byte is twice that of
+// 16 rows.
 //
 // XL: the workgroup's activation rows (whole K) are staged in LDS once, at
 // the start, and each step's B operand is read from there. The only vector
@@ -150,7 +156,10 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
   constexpr int NLD = 16 * NT / RPI; // load instructions per chunk
   constexpr int NSUB = kWaves / KW;  // row groups a workgroup works on at once
   constexpr int SWZ = (LPR < 16 ? LPR : 16) - 1;  // position swizzle stays inside a row
-  constexpr int TILE = 16 * NT * LPR * 16;  // bytes of one wave's LDS tile
+  // DIRECT: each lane loads its own A operand (row l % 16, 16 bytes at
+  // k = 64 step + 16 (l / 16)) straight from HBM, no LDS tile
+  constexpr bool DIRECT = XL && MT >= 2;
+  constexpr int TILE = DIRECT ? 16 : 16 * NT * LPR * 16;  // bytes of one wave's LDS tile
   __shared__ __attribute__((aligned(16))) char wtile[kWaves][TILE];
   __shared__ __attribute__((aligned(16))) float red[KW > 1 ? KW - 1 : 1][NT * MT * 4][64];
   extern __shared__ __attribute__((aligned(16))) char xsm[];  // XL: activation rows
@@ -237,10 +246,23 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
     const int s0 = ks + c * U;
     const int64_t kw_off = static_cast<int64_t>(min(s0 + ld_step, p.nks - 1)) * 64 +
                            (ld_unit & 3) * 16;
+    if constexpr (DIRECT) {
+    (void)kw_off;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = min(n0 + nt * 16 + lr, p.N - 1);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t ko = static_cast<int64_t>(min(s0 + u, p.nks - 1)) * 64 + lg * 16;
+        R.w[nt * U + u] = sd::load16_stream(real ? p.w + static_cast<int64_t>(n) * p.ws + ko : p.w);
+      }
+    }
+    } else {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int n = min(n0 + i * RPI + ld_row, p.N - 1);
       R.w[i] = sd::load16_stream(real ? p.w + static_cast<int64_t>(n) * p.ws + kw_off : p.w);
+    }
     }
 #pragma unroll
     for (int u = 0; u < (XL ? 0 : U); ++u) {
@@ -270,12 +292,14 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
     const int n0 = g * NT * 16;
     const int s0 = ks + c * U;
     // stage: row r = i * RPI + ld_row, unit ld_unit at position ld_unit ^ (r & 15)
+    if constexpr (!DIRECT) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int r = i * RPI + ld_row;
       sd::store16(tile + (r * LPR + (ld_unit ^ (r & SWZ))) * 16, R.w[i]);
     }
     sd::wave_lds_sync();
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int step = s0 + u;
@@ -304,7 +328,9 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int r = nt * 16 + lr;
-        const u32x4 wv = sd::load16(tile + (r * LPR + ((u * 4 + lg) ^ (r & SWZ))) * 16);
+        u32x4 wv;
+        if constexpr (DIRECT) wv = R.w[nt * U + u];
+        else wv = sd::load16(tile + (r * LPR + ((u * 4 + lg) ^ (r & SWZ))) * 16);
         const u32x4 a0 = dequant8<T>(wv.x, wv.y);  // k = 16 lg + 0..7
         const u32x4 a1 = dequant8<T>(wv.z, wv.w);  // k = 16 lg + 8..15
         if constexpr (!PER_GROUP) {
@@ -337,7 +363,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
         }
       }
     }
-    sd::wave_lds_sync();  // every lane has read the tile before the next chunk overwrites it
+    if constexpr (!DIRECT) sd::wave_lds_sync();  // every lane has read the tile before the next chunk overwrites it
   };
 
   // lane holds y^T[n = n0 + 16 nt + 4 lg + i][m = m0 + 16 mt + lr]
@@ -799,9 +825,9 @@ int w8_lds_per_block() {
 
 // Static LDS of w8a16_kernel<.., MT, NT, KW, U, ..>: the weight tiles and the
 // K-split reduction slot, as the kernel declares them.
-template <int MT, int NT, int KW, int U>
+template <int MT, int NT, int KW, int U, bool XL>
 constexpr size_t w8_static_lds() {
-  return static_cast<size_t>(kWaves) * (16 * NT * 4 * U * 16) +
+  return static_cast<size_t>(kWaves) * (XL && MT >= 2 ? 16 : 16 * NT * 4 * U * 16) +
          static_cast<size_t>(KW > 1 ? KW - 1 : 1) * (NT * MT * 4) * 64 * 4;
 }
 
@@ -815,9 +841,11 @@ int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
     const size_t xbytes = static_cast<size_t>(rows) * p.xpitch;
     const size_t xmax = static_cast<size_t>(KW == 1 ? kXlMaxBytes : kXlMaxBytesSplit);
     if (p.xpitch > 0 && xbytes <= xmax && (KW == 1 || MODE != 0 || p.M > 16)) {
-      // 32 staged rows leave LDS for one workgroup per CU: 8-step chunks (16 KB
-      // per wave at NT = 2) keep enough of the weight stream in flight
-      constexpr int UX = MT >= 2 ? 8 : U;
+      // 32 staged rows (MT = 2) load the weights straight into MFMA operand
+      // order, no weight tile: two workgroups per CU fit beside the rows, and
+      // 2-step chunks measured best there (lm_head M = 56: 63.8 us; 8-step
+      // chunks through the tile at one workgroup per CU: 77.8 us)
+      constexpr int UX = MT >= 2 ? 2 : U;
       constexpr int NSUB = kWaves / KW;
       auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true, MODE>;
       // occupancy from the activation rows; the scale table adds a few KB (per
@@ -831,7 +859,7 @@ int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
       q.ngmax = (p.groups + static_cast<int>(grid.x) * NSUB - 1) / (static_cast<int>(grid.x) * NSUB);
       const size_t spr = PG ? static_cast<size_t>(p.K / p.group) : 1;
       const size_t tbl = static_cast<size_t>(NSUB) * q.ngmax * NT * 16 * (spr + (p.bias ? 1 : 0)) * 4;
-      const size_t lds = w8_static_lds<MT, NT, KW, UX>() + q.xbytes + tbl;
+      const size_t lds = w8_static_lds<MT, NT, KW, UX, true>() + q.xbytes + tbl;
       if (tbl <= static_cast<size_t>(kXlScaleBytes) &&
           lds <= static_cast<size_t>(w8_lds_per_block())) {
         hipLaunchKernelGGL(kern, grid, dim3(kThreads), q.xbytes + tbl, st, q);

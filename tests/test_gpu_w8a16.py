@@ -75,7 +75,7 @@ def test_ragged_shapes_and_bias(M, N, K):
     check(y, c["x"], c["w"], c["s"], bias, what=f"{M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("M", [1, 3, 12])
+@pytest.mark.parametrize("M", [1, 3, 12, 40])
 @pytest.mark.parametrize("gs", [0, 64, 128])
 def test_wide_path_scales_and_bias(M, gs):
     # N = 33000 rows of K = 1024: the wide path (whole rows per wave, activation rows and
@@ -193,7 +193,8 @@ def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
                                               (40, 1024, 1024, 0, torch.bfloat16, True),
                                               (3, 512, 1152, 0, torch.float16, True),
                                               (2, 1024, 8192, 0, torch.bfloat16, False),
-                                              (9, 33000, 1024, 128, torch.float16, True)])
+                                              (9, 33000, 1024, 128, torch.float16, True),
+                                              (24, 33000, 1024, 0, torch.bfloat16, True)])
 def test_rmsnorm_linear_is_rmsnorm_then_linear(M, N, K, gs, act, res):
     # add + RMSNorm formed while staging: bit-identical to rmsnorm then the
     # linear, residual_out identical to rmsnorm's (one row block per 16 or 32
