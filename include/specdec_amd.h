@@ -197,6 +197,8 @@ size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_si
  * whole weight rows through fp32 FMAs; other shapes run the MFMA kernel (the
  * SiLU and RMSNorm forms below follow the same rule). Supported: K % 64 == 0,
  * group_size 0 or a multiple of 64 dividing K. `workspace` may be NULL.
+ * y may share no byte with x (SD_ERR_VALUE): other workgroups still read x
+ * while one writes y.
  */
 int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t w_stride_n,
                     const void* scale, int32_t scale_dtype, int32_t group_size,
@@ -212,7 +214,8 @@ int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t 
  * the fusion saves the SiluAndMul launch and its round trip through memory.
  * The activation equals sd_silu_mul's output bit for bit, so y equals
  * sd_silu_mul followed by sd_w8a16_linear. gate_up: (M, >= 2K) dtype, row
- * stride gate_up_stride_m; the rest as sd_w8a16_linear (no workspace). On the
+ * stride gate_up_stride_m, sharing no byte with y; the rest as
+ * sd_w8a16_linear (no workspace). On the
  * row-streaming path (one or two rows, see sd_w8a16_linear) each wave forms
  * the SiLU of its columns once; otherwise it is computed once per workgroup
  * while its activation rows are staged in LDS, which holds while
@@ -234,8 +237,9 @@ int sd_w8a16_silu_linear(const void* gate_up, int64_t gate_up_stride_m, const in
  * trip through memory. The normalised row equals sd_rmsnorm's out bit for bit,
  * so y equals sd_rmsnorm followed by sd_w8a16_linear; with a residual,
  * residual_out (may be NULL) receives bf16(x + residual) as sd_rmsnorm's
- * residual_out does, written by one workgroup per row block. residual_out may
- * alias neither x nor residual (other workgroups still read them). On the
+ * residual_out does, written by one workgroup per row block. residual_out and
+ * y may share no byte with x, residual or each other (other workgroups still
+ * read the inputs): SD_ERR_VALUE. On the
  * row-streaming path (one or two rows, see sd_w8a16_linear) every wave forms
  * the norm of its columns; otherwise each workgroup normalises its activation
  * rows, one after another, while staging them in LDS. The form pays for a few

@@ -836,20 +836,6 @@ struct Plan {
   int64_t slots;  // partial slots: (runs + num_seqs) * Hkv
 };
 
-// Compute units of the current device (cached per device id).
-int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      n <= 0)
-    n = 256;
-  if (dev >= 0 && dev < 64) cache[dev] = n;
-  return n;
-}
-
 // num_splits == 0: one resident set of waves (4 SIMDs x main_occupancy per
 // compute unit, one wave per kv head of a run) shares all the columns, at
 // least one column (two for two row tiles) per run.
@@ -870,7 +856,7 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
     pl.min_steps = 1;
   } else {
     const int occ = pl.RT == 1 ? main_occupancy<1>() : main_occupancy<2>();
-    runs = static_cast<int64_t>(device_cus()) * 4 * occ / (Hkv * pl.KS);
+    runs = static_cast<int64_t>(sd::device_cus()) * 4 * occ / (Hkv * pl.KS);
     pl.min_steps = pl.RT == 1 || pl.KS == 2 ? 1 : 2;  // at least 64 keys per run with two tiles
   }
   const int groups = Hkv / (pl.NW / pl.KS);

@@ -240,6 +240,24 @@ void clear_error();
 // Maps a pending HIP launch error into SD_ERR_HIP with `what` in the message.
 int check_launch(const char* what);
 
+// Compute units / LDS bytes per workgroup of the current device, cached per
+// device id (safe to call from several host threads at once).
+int device_cus();
+int device_lds_per_block();
+
+// Byte range [lo, hi) of a row-major 16-bit matrix (rows x width, row stride
+// in elements); empty for a NULL pointer or no rows.
+struct Span {
+  uintptr_t lo, hi;
+  bool overlaps(const Span& o) const { return lo < hi && o.lo < o.hi && lo < o.hi && o.lo < hi; }
+};
+inline Span span16(const void* p, int64_t rows, int64_t stride, int64_t width) {
+  if (!p || rows <= 0 || width <= 0) return Span{0, 0};
+  const int64_t st = stride > 0 ? stride : 0;
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+  return Span{lo, lo + static_cast<uintptr_t>(((rows - 1) * st + width) * 2)};
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace sd

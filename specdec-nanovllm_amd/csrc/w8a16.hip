@@ -710,20 +710,6 @@ struct W8Plan {
   int MT, NT, KW, mblocks, groups, grid;
 };
 
-// Compute units of the current device (cached per device id).
-int w8_device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      n <= 0)
-    n = 256;
-  if (dev >= 0 && dev < 64) cache[dev] = n;
-  return n;
-}
-
 W8Plan make_plan(int64_t M, int64_t N, int64_t K) {
   W8Plan pl;
   // Activation rows in blocks of 16 (MT = 1) or 32 (MT = 2) along grid.y: a
@@ -734,7 +720,7 @@ W8Plan make_plan(int64_t M, int64_t N, int64_t K) {
   pl.MT = M <= 16 ? 1 : 2;
   pl.mblocks = static_cast<int>((M + pl.MT * 16 - 1) / (pl.MT * 16));
   const int64_t nr = (N + 15) / 16;
-  const int cus = w8_device_cus();
+  const int cus = sd::device_cus();
   const int64_t nks = K / 64;
   // Enough 16-row tiles for ~8 waves per CU: every wave owns whole rows, two
   // tiles at a time. Otherwise four waves split K of one tile (16 activation
@@ -809,20 +795,6 @@ int resident_wgs_xl(Kern kern, size_t smem) {
   return resident_wgs_of(reinterpret_cast<const void*>(kern), smem);
 }
 
-// LDS bytes one workgroup may use on the current device (cached per device id).
-int w8_lds_per_block() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
-      n <= 0)
-    n = 65536;
-  if (dev >= 0 && dev < 64) cache[dev] = n;
-  return n;
-}
-
 // Static LDS of w8a16_kernel<.., MT, NT, KW, U, ..>: the weight tiles and the
 // K-split reduction slot, as the kernel declares them.
 template <int MT, int NT, int KW, int U, bool XL>
@@ -850,7 +822,7 @@ int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
       auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true, MODE>;
       // occupancy from the activation rows; the scale table adds a few KB (per
       // channel: 16 B per row of the workgroup)
-      unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs_xl(kern, xbytes)) /
+      unsigned cap = static_cast<unsigned>(sd::device_cus() * resident_wgs_xl(kern, xbytes)) /
                      grid.y;
       cap = cap >= 8 ? cap / 8 * 8 : 1;
       if (grid.x > cap) grid.x = cap;
@@ -861,7 +833,7 @@ int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
       const size_t tbl = static_cast<size_t>(NSUB) * q.ngmax * NT * 16 * (spr + (p.bias ? 1 : 0)) * 4;
       const size_t lds = w8_static_lds<MT, NT, KW, UX, true>() + q.xbytes + tbl;
       if (tbl <= static_cast<size_t>(kXlScaleBytes) &&
-          lds <= static_cast<size_t>(w8_lds_per_block())) {
+          lds <= static_cast<size_t>(sd::device_lds_per_block())) {
         hipLaunchKernelGGL(kern, grid, dim3(kThreads), q.xbytes + tbl, st, q);
         return SD_OK;
       }
@@ -877,7 +849,7 @@ int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
     // exactly one resident set of workgroups over all activation blocks (a
     // partial second round would leave most of the GPU idle at the end), grid.x
     // a multiple of 8 so that block (x, y) shares an XCD (and its L2) with (x, 0)
-    unsigned cap = static_cast<unsigned>(w8_device_cus() * resident_wgs(kern)) / grid.y;
+    unsigned cap = static_cast<unsigned>(sd::device_cus() * resident_wgs(kern)) / grid.y;
     cap = cap >= 8 ? cap / 8 * 8 : 1;
     if (grid.x > cap) grid.x = cap;
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, p);
@@ -931,7 +903,7 @@ bool rows_eligible(const W8Params& p) {
 template <typename T, int MR, int C, int MODE>
 int launch_rows_c(const W8Params& p, hipStream_t st) {
   // about 4 rows per wave, at most two waves per SIMD (8 per CU)
-  int64_t waves = static_cast<int64_t>(w8_device_cus()) * 8;
+  int64_t waves = static_cast<int64_t>(sd::device_cus()) * 8;
   const int64_t want = (static_cast<int64_t>(p.N) + 3) / 4;
   if (want < waves) waves = want;
   const int blocks = static_cast<int>((waves + kWaves - 1) / kWaves);
@@ -1038,6 +1010,19 @@ int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& nor
     sd::set_error("w8a16: x and w rows (and the up half) must be 16-byte aligned");
     return SD_ERR_UNSUPPORTED;
   }
+  // Other workgroups read x / residual while a workgroup writes y and
+  // residual_out, so no output may share a byte with an input or with the
+  // other output.
+  const int64_t xw = up >= 0 ? up + K : K;
+  const sd::Span sx = sd::span16(x, M, x_stride_m, xw), sy = sd::span16(y, M, y_stride_m, N);
+  const sd::Span sr = sd::span16(norm.residual, M, norm.residual_stride, K);
+  const sd::Span sro = sd::span16(norm.residual_out, M, norm.residual_out_stride, K);
+  if (sy.overlaps(sx) || sy.overlaps(sr) || sy.overlaps(sro) || sro.overlaps(sx) ||
+      sro.overlaps(sr)) {
+    sd::set_error("w8a16: y / residual_out overlap an input or each other (other workgroups "
+                  "still read the inputs)");
+    return SD_ERR_VALUE;
+  }
   const W8Plan pl = make_plan(M, N, K);
   W8Params p;
   p.x = static_cast<const uint16_t*>(x);
@@ -1126,11 +1111,6 @@ extern "C" int sd_w8a16_rmsnorm_linear(const void* x, int64_t x_stride_m, const 
     sd::set_error("w8a16_rmsnorm: needs the norm weight and K a multiple of 8 up to 8192 (K=%lld)",
                   (long long)K);
     return SD_ERR_UNSUPPORTED;
-  }
-  if (residual && residual_out && (residual == residual_out || residual_out == x)) {
-    sd::set_error("w8a16_rmsnorm: residual_out may not alias the residual or x (other "
-                  "workgroups still read them)");
-    return SD_ERR_VALUE;
   }
   if ((residual && (!sd::aligned16(residual) || residual_stride_m % 8)) ||
       (residual_out && (!sd::aligned16(residual_out) || residual_out_stride_m % 8)) ||

@@ -316,7 +316,8 @@ def w8a16_rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     """w8a16_linear(rmsnorm(x, norm_weight, eps, residual)[0], ...): a decoder
     layer's RMSNorm (layers/layernorm.py:16-47) feeding the next projection.
     The normalised rows equal ``rmsnorm``'s bit for bit. With ``residual``,
-    ``residual_out`` (aliasing neither x nor residual; None: not written)
+    ``residual_out`` (sharing no byte with x, residual or the output; None:
+    not written)
     receives bf16(x + residual), ``rmsnorm``'s second output. One launch for
     up to 4 rows: at one or two rows every wave of the row-streaming GEMV
     forms the norm of its columns; at three or four the tiled kernel's

@@ -124,3 +124,32 @@ def test_ops_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.w8a16_linear(torch.zeros((1, 64), dtype=torch.float16),
                          torch.zeros((8, 64), dtype=torch.int8), torch.ones(8))
+
+
+def test_w8a16_rejects_overlapping_outputs():
+    """Other workgroups still read x / residual while one writes y or
+    residual_out, so any shared byte is refused before a launch."""
+    lib = _lib.load()
+    M, N, K = 2, 4096, 1024
+    x, res, w, s, nw = 0x100000, 0x200000, 0x300000, 0x400000, 0x500000
+    row = K * 2
+
+    def norm_call(res_out, y):
+        return lib.sd_w8a16_rmsnorm_linear(x, K, res, K, res_out, K, nw, 1e-6, w, K, s,
+                                           _lib.SD_BF16, 0, None, y, N, M, N, K,
+                                           _lib.SD_BF16, None)
+
+    free = 0x600000
+    # residual_out: partly over the second row of x, or over the residual's tail
+    assert norm_call(x + row, free) == _lib.SD_ERR_VALUE
+    assert b"overlap" in lib.sd_last_error()
+    assert norm_call(res + row + 512, free) == _lib.SD_ERR_VALUE
+    # y over x, over the residual, or over residual_out
+    assert norm_call(free, x + 16) == _lib.SD_ERR_VALUE
+    assert norm_call(free, res - 16) == _lib.SD_ERR_VALUE
+    assert norm_call(free, free + 2 * row - 16) == _lib.SD_ERR_VALUE
+    # plain and SiLU forms: y over the activation rows
+    assert lib.sd_w8a16_linear(x, K, w, K, s, _lib.SD_BF16, 0, None, x + row, N, M, N, K,
+                               _lib.SD_BF16, None, 0, None) == _lib.SD_ERR_VALUE
+    assert lib.sd_w8a16_silu_linear(x, 2 * K, w, K, s, _lib.SD_BF16, 0, None, x + 3 * row, N,
+                                    M, N, K, _lib.SD_BF16, None) == _lib.SD_ERR_VALUE

@@ -258,8 +258,14 @@ def test_rmsnorm_linear_rejects_aliased_residual():
     x = torch.randn((M, K), device=DEV).to(torch.bfloat16)
     r = torch.randn((M, K), device=DEV).to(torch.bfloat16)
     nw = torch.ones((K,), device=DEV, dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="alias"):
+    with pytest.raises(ValueError, match="overlap"):
         ops.w8a16_rmsnorm_linear(x, nw, 1e-6, c["w"], c["s"], residual=r, residual_out=r)
+    # a partial overlap (residual_out starting at the second row of x) is refused too
+    buf = torch.empty((3, K), device=DEV, dtype=torch.bfloat16)
+    buf[:2] = x
+    with pytest.raises(ValueError, match="overlap"):
+        ops.w8a16_rmsnorm_linear(buf[:2], nw, 1e-6, c["w"], c["s"], residual=r,
+                                 residual_out=buf[1:3])
 
 
 @pytest.mark.parametrize("M", [1, 2])
