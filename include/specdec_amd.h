@@ -120,6 +120,34 @@ int sd_paged_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
                        void* stream);
 
 /*
+ * sd_paged_attention without the workspace arguments, allocating nothing: the
+ * split-KV workspace is the library's static device scratch (one per device,
+ * SD_NOALLOC_SCRATCH_BYTES, held from the first call on that device until the
+ * process ends). No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same kernels, plan and results as
+ * sd_paged_attention with a workspace (bit for bit). Sizes whose workspace
+ * (sd_paged_attention_workspace_size) exceeds the scratch return
+ * SD_ERR_UNSUPPORTED. Every call on a device shares that device's scratch:
+ * calls that overlap in time on one device (two streams, two threads) race and
+ * must be ordered by the caller. Nothing needs clearing between calls (every
+ * partial the merge reads is written earlier in the same call).
+ */
+#define SD_NOALLOC_SCRATCH_BYTES (32u << 20)
+int sd_paged_attention_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                               const void* k_cache, const void* v_cache,
+                               int64_t cache_stride_block, int64_t cache_stride_pos,
+                               int64_t cache_stride_head, int64_t num_blocks,
+                               int32_t block_size, const int32_t* block_table,
+                               int64_t bt_stride, int32_t max_blocks_per_seq,
+                               const int32_t* context_lens, const int32_t* cu_seqlens_k,
+                               const int32_t* cu_seqlens_q, int32_t max_qlen,
+                               int64_t total_q, int32_t num_seqs, int32_t num_q_heads,
+                               int32_t num_kv_heads, int32_t head_dim, float scale,
+                               int32_t dtype, void* out, int64_t out_stride_tok,
+                               int64_t out_stride_head, int32_t num_splits, void* stream);
+
+/*
  * Same arguments as sd_paged_attention, but only the split-KV main kernel
  * runs: `out` receives the rows of (sequence, kv head) pairs that one
  * workgroup covered and the workspace the partial (m, l, acc) of the others;

@@ -50,6 +50,8 @@
 // to their slots. The hot loop of the store launch is the plain one.
 #include <math.h>
 
+#include <atomic>
+
 #include "sd_common.h"
 
 namespace {
@@ -922,6 +924,40 @@ struct NewRows {  // fused store_kvcache arguments (key == NULL: none)
   const int32_t* slot_mapping;
 };
 
+// Scratch of sd_paged_attention_noalloc: the split-KV workspace in a static
+// device array (each device holds its own copy from the library's load until
+// the process ends). Host code never passes `scratch` itself to a kernel: the
+// host-side name is a stand-in, not a device address. The per-device address
+// comes from hipGetSymbolAddress (scratch_address below).
+constexpr size_t kScratchBytes = SD_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxScratchDevices];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (a racing second lookup stores the same address).
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    sd::set_error("paged_attention_noalloc: no current device below %d", kMaxScratchDevices);
+    return SD_ERR_HIP;
+  }
+  void* ptr = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      sd::set_error("paged_attention_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                    hipGetErrorString(e));
+      return SD_ERR_HIP;
+    }
+    g_scratch_addr[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return SD_OK;
+}
+
+// static_scratch: the workspace is this device's `scratch` (sd_paged_attention_noalloc)
 int run_attention(bool combine, const NewRows& nr, const void* q, int64_t q_stride_tok,
                   int64_t q_stride_head,
                   const void* k_cache, const void* v_cache, int64_t cache_stride_block,
@@ -932,7 +968,8 @@ int run_attention(bool combine, const NewRows& nr, const void* q, int64_t q_stri
                   int64_t total_q, int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                   int32_t head_dim, float scale, int32_t dtype, void* out,
                   int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
-                  size_t workspace_bytes, int32_t num_splits, void* stream) {
+                  size_t workspace_bytes, int32_t num_splits, void* stream,
+                  bool static_scratch = false) {
   sd::clear_error();
   if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
       block_size <= 0 || num_blocks <= 0 || max_blocks_per_seq <= 0 || max_qlen <= 0 ||
@@ -1002,6 +1039,17 @@ int run_attention(bool combine, const NewRows& nr, const void* q, int64_t q_stri
   }
   const Plan pl = make_plan(num_seqs, max_qlen, num_q_heads, num_kv_heads, num_splits);
   const size_t need = ws_bytes(pl);
+  if (static_scratch) {
+    if (need > kScratchBytes) {
+      sd::set_error("paged_attention_noalloc: these sizes need %zu bytes of scratch, more than "
+                    "the %zu of the static scratch (call sd_paged_attention with a workspace)",
+                    need, kScratchBytes);
+      return SD_ERR_UNSUPPORTED;
+    }
+    const int rc = scratch_address(&workspace);
+    if (rc != SD_OK) return rc;
+    workspace_bytes = kScratchBytes;
+  }
   if (!workspace || workspace_bytes < need || !sd::aligned16(workspace)) {
     sd::set_error("paged_attention: workspace of %zu bytes (16-byte aligned) required, got %zu",
                   need, workspace ? workspace_bytes : (size_t)0);
@@ -1091,6 +1139,23 @@ extern "C" int sd_paged_attention(
                        cu_seqlens_k, cu_seqlens_q, max_qlen, total_q, num_seqs, num_q_heads,
                        num_kv_heads, head_dim, scale, dtype, out, out_stride_tok,
                        out_stride_head, workspace, workspace_bytes, num_splits, stream);
+}
+
+extern "C" int sd_paged_attention_noalloc(
+    const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+    const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_pos,
+    int64_t cache_stride_head, int64_t num_blocks, int32_t block_size,
+    const int32_t* block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+    const int32_t* context_lens, const int32_t* cu_seqlens_k, const int32_t* cu_seqlens_q,
+    int32_t max_qlen, int64_t total_q, int32_t num_seqs, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, float scale, int32_t dtype, void* out,
+    int64_t out_stride_tok, int64_t out_stride_head, int32_t num_splits, void* stream) {
+  return run_attention(true, NewRows{}, q, q_stride_tok, q_stride_head, k_cache, v_cache,
+                       cache_stride_block, cache_stride_pos, cache_stride_head, num_blocks,
+                       block_size, block_table, bt_stride, max_blocks_per_seq, context_lens,
+                       cu_seqlens_k, cu_seqlens_q, max_qlen, total_q, num_seqs, num_q_heads,
+                       num_kv_heads, head_dim, scale, dtype, out, out_stride_tok,
+                       out_stride_head, nullptr, 0, num_splits, stream, true);
 }
 
 extern "C" int sd_paged_attention_partial(

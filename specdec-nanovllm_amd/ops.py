@@ -89,7 +89,8 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
                     layout: str = "interleaved", num_splits: int = 0,
                     out: torch.Tensor | None = None, main_only: bool = False,
                     key: torch.Tensor | None = None, value: torch.Tensor | None = None,
-                    slot_mapping: torch.Tensor | None = None) -> torch.Tensor:
+                    slot_mapping: torch.Tensor | None = None,
+                    no_alloc: bool = False) -> torch.Tensor:
     """Paged decode (``cu_seqlens_q is None``: one query row per sequence) or
     speculative-verify attention (rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]``,
     bottom-right causal), GQA, split-KV.
@@ -105,6 +106,11 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     rounding (the new keys are scored in fp32 in the merge launch), for the
     engine's slot layout: sequence b's rows are its last n_b keys (slot -1: not
     written).
+
+    ``no_alloc`` runs the same kernels on the library's static device scratch
+    (``sd_paged_attention_noalloc``) instead of a workspace from torch's
+    allocator; pass ``out`` as well to allocate nothing at all. Calls that
+    overlap in time on one device share that scratch and race.
     """
     if q.dim() != 3:
         raise ValueError(f"q must be (tokens, heads, head_dim), got {tuple(q.shape)}")
@@ -136,6 +142,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     else:
         assert out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
     fused = key is not None
+    assert not (no_alloc and (fused or main_only)), "no_alloc is the plain attention call"
     if fused:
         assert value is not None and slot_mapping is not None and not main_only
         assert key.shape == (total_q, num_kv_heads, head_dim) and value.shape == key.shape
@@ -154,6 +161,19 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         fn = lib.sd_paged_attention_store
         new_rows = (key.data_ptr(), key.stride(0), key.stride(1),
                     value.data_ptr(), value.stride(0), value.stride(1), slots.data_ptr())
+    if no_alloc:
+        with torch.cuda.device(dev):
+            rc = lib.sd_paged_attention_noalloc(
+                q.data_ptr(), q.stride(0), q.stride(1),
+                k_cache.data_ptr(), v_cache.data_ptr(), sb, sp, sh, num_blocks,
+                block_size, bt.data_ptr(), bt.stride(0), max_blocks,
+                _ptr(ctx), _ptr(cuk), _ptr(cuq),
+                int(max_seqlen_q), total_q, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                float(scale), _lib.dtype_code(q.dtype),
+                out.data_ptr(), out.stride(0), out.stride(1), int(num_splits),
+                _lib.stream_ptr(dev))
+        _lib.check(rc)
+        return out
     with torch.cuda.device(dev):
         # the plan (and so the workspace) depends on the device's compute units
         ws_bytes = lib.sd_paged_attention_workspace_size(
