@@ -260,10 +260,66 @@ def bench_verify(ops, workloads, torch, steps, cpu_seconds=0.0):
               + case["slots"].numel() * 8 * 128 * 2 * 2 * 2)
     flops = sum(4 * 32 * 128 * (case["k"] + 1) * int(L) for L in case["keys"])
     res = {"config": "C3 verify B=8 q_len 7 (store + attention)", "us": round(ms * 1e3, 2),
-           "GBps": round(nbytes / ms / 1e6, 1), "TFLOPs": round(flops / ms / 1e9, 2),
-           "seed": case["seed_used"]}
+           "GBps": round(nbytes / ms / 1e6, 1), "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
+           "TFLOPs": round(flops / ms / 1e9, 2), "seed": case["seed_used"]}
+    # the plain (non-storing) call and its twins over the same keys
+    ws_bytes = ops.paged_attention_workspace_bytes(8, case["k"] + 1, 32, 8, bt.shape[1] * 256,
+                                                   device=dev)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    for twin in (None, "main", "floor"):
+        def call(twin=twin):
+            ops.paged_attention(case["q"], case["k_cache"], case["v_cache"], bt, case["scale"],
+                                cu_seqlens_k=cuk, cu_seqlens_q=cuq, max_seqlen_q=case["k"] + 1,
+                                out=out, twin=twin, workspace=ws)
+        t = time_replays([graph_of(call, torch)], steps, 10, torch)
+        res[{None: "attention_us", "main": "main_us", "floor": "floor_us"}[twin]] = \
+            round(t * 1e3, 2)
     if cpu_seconds > 0:
         res["cpu_baseline"] = cpu_baseline_verify(case, cpu_seconds)
+    return res
+
+
+def bench_decode_batch(ops, workloads, torch, B, steps):
+    """C2 decode step (fused store + attention) at batch B over disjoint page
+    sets, one graph of consecutive steps; plus the attention main kernel and its
+    read-only floor over the same sets."""
+    probe = workloads.decode_case(B, seed=B, sets=1, device="cpu", num_blocks=2048,
+                                  num_q_heads=1, num_kv_heads=1, head_dim=8)
+    pages = sum(math.ceil(int(L) / 256) for L in probe["lens"])
+    sets = max(1, min(16, 2048 // pages))
+    case = workloads.decode_case(B, seed=B, sets=sets)
+    lens_d = case["lens"].cuda()
+    tables = [t.cuda() for t in case["tables"]]
+    slots = [x.cuda() for x in case["slots"]]
+    out = torch.empty_like(case["q"])
+    ws_bytes = ops.paged_attention_workspace_bytes(B, 1, 32, 8, tables[0].shape[1] * 256,
+                                                   device="cuda")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+
+    def chain(**kw):
+        fns = [lambda i=i: ops.paged_attention(case["q"], case["k_cache"], case["v_cache"],
+                                               tables[i], case["scale"], context_lens=lens_d,
+                                               out=out, **({"key": case["k_new"],
+                                                            "value": case["v_new"],
+                                                            "slot_mapping": slots[i]}
+                                                           if kw.get("store") else
+                                                           {"twin": kw.get("twin"),
+                                                            "workspace": ws}))
+               for i in range(sets)]
+        return lambda: [f() for f in fns]
+    reps = max(2, steps // sets)
+    res = {"config": f"C2 decode step B={B} (store + attention), {sets} page sets"}
+    for name, kw in (("step_us", {"store": True}), ("attention_us", {}),
+                     ("main_us", {"twin": "main"}), ("floor_us", {"twin": "floor"})):
+        g = graph_of(chain(**kw), torch)
+        res[name] = round(time_replays([g], reps, 2, torch) / sets * 1e3, 2)
+        del g
+    nbytes = decode_bytes(case["lens"].tolist(), 32, 8, 128, 2, B)
+    res["GBps"] = round(nbytes / res["step_us"] / 1e3, 1)
+    res["frac"] = round(res["GBps"] / PEAK_HBM_GBS, 4)
+    res["algorithmic_bytes"] = nbytes
+    del case
+    torch.cuda.empty_cache()
     return res
 
 
@@ -470,6 +526,22 @@ def main():
         return lambda: ops.paged_attention(q, kc, vc, tables[i], case["scale"],
                                            context_lens=lens_d, out=out)
 
+    # measurement twins: the main kernel's loads alone (read-only floor), and the
+    # merge alone over the workspace a main-only call left for each page set
+    ws_bytes = ops.paged_attention_workspace_bytes(B, 1, hq, hkv,
+                                                   tables[0].shape[1] * 256, device="cuda")
+    twin_ws = [torch.empty(ws_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
+
+    def floor_fn(i):
+        return lambda: ops.paged_attention(q, kc, vc, tables[i], case["scale"],
+                                           context_lens=lens_d, out=out, twin="floor",
+                                           workspace=twin_ws[i])
+
+    def combine_fn(i):
+        return lambda: ops.paged_attention(q, kc, vc, tables[i], case["scale"],
+                                           context_lens=lens_d, out=out, twin="combine",
+                                           workspace=twin_ws[i])
+
     step_graphs = [graph_of(step_fn(i), torch) for i in range(sets)]
 
     def chain(make):
@@ -479,6 +551,11 @@ def main():
         return lambda: [f() for f in fns]
     main_graphs = [graph_of(chain(main_fn), torch)]
     attn_graphs = [graph_of(chain(attn_fn), torch)]
+    floor_graphs = [graph_of(chain(floor_fn), torch)]
+    for i in range(sets):  # fill each set's workspace once for the combine twin
+        ops.paged_attention(q, kc, vc, tables[i], case["scale"], context_lens=lens_d, out=out,
+                            twin="main", workspace=twin_ws[i])
+    combine_graphs = [graph_of(chain(combine_fn), torch)]
     step_chain = graph_of(chain(step_fn), torch)
 
     # ---- timed region: exactly `steps` decode steps (each a full fused store +
@@ -494,6 +571,8 @@ def main():
     reps = max(1, args.steps // sets)
     ms_main = time_replays(main_graphs, reps, max(1, args.warmup // sets), torch) / sets
     ms_attn = time_replays(attn_graphs, reps, max(1, args.warmup // sets), torch) / sets
+    ms_floor = time_replays(floor_graphs, reps, max(1, args.warmup // sets), torch) / sets
+    ms_comb = time_replays(combine_graphs, reps, max(1, args.warmup // sets), torch) / sets
     a_bytes = attn_bytes(lens.tolist(), hq, hkv, d, 2)
     achieved = a_bytes / (ms_main * 1e-3) / 1e9
 
@@ -514,19 +593,31 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": load_traffic("paged_attn_main_c2_b32"),
                      "kernel": "paged_attn_main", "algorithmic_bytes": a_bytes,
-                     "avg_us": round(ms_main * 1e3, 2)},
+                     "avg_us": round(ms_main * 1e3, 2),
+                     "floor_us": round(ms_floor * 1e3, 2),
+                     "floor_note": "sd_paged_attention_floor: the same grid, loads and "
+                                   "prefetch with no math (the access pattern's time)",
+                     "traffic_note": "bytes per launch from the committed rocprofv3 "
+                                     "FETCH_SIZE/WRITE_SIZE passes (profiles/traffic.json), "
+                                     "not measured in this run"},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds, torch)
     if not args.no_extra:
-        del step_graphs, main_graphs, attn_graphs, step_chain
+        del step_graphs, main_graphs, attn_graphs, step_chain, floor_graphs, combine_graphs
+        del twin_ws
         extra = {"attention_op_us": round(ms_attn * 1e3, 2),
                  "attention_main_us": round(ms_main * 1e3, 2),
+                 "attention_combine_us": round(ms_comb * 1e3, 2),
+                 "attention_floor_us": round(ms_floor * 1e3, 2),
                  "step_us": round(ms_step * 1e3, 2),
                  "step_us_one_graph_per_step": round(ms_step_graph * 1e3, 2)}
         del case, kc, vc
         torch.cuda.empty_cache()
         cpu_s = 0.0 if args.no_cpu_baseline else max(args.cpu_seconds / 2, 1.0)
+        extra["decode_batches"] = [bench_decode_batch(ops, workloads, torch, b, args.steps)
+                                   for b in (1, 8)]
+        torch.cuda.empty_cache()
         extra["verify"] = bench_verify(ops, workloads, torch, args.steps, cpu_s)
         torch.cuda.empty_cache()
         extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100))

@@ -170,6 +170,50 @@ int sd_paged_attention_partial(const void* q, int64_t q_stride_tok, int64_t q_st
                                int32_t num_splits, void* stream);
 
 /*
+ * Same arguments as sd_paged_attention, but only the merge kernel runs, over
+ * the workspace that a sd_paged_attention_partial call with the same
+ * arguments filled (stream-ordered before it): the rows of shared pairs and
+ * the zero rows of sequences without keys are written to `out`. Together the
+ * two calls give sd_paged_attention's result. Measurement twin of
+ * `paged_decode_cuda_combine` (nanovllm/kernels/paged_decode_attn_cuda.cu:1544-1555).
+ */
+int sd_paged_attention_combine(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                               const void* k_cache, const void* v_cache,
+                               int64_t cache_stride_block, int64_t cache_stride_pos,
+                               int64_t cache_stride_head, int64_t num_blocks,
+                               int32_t block_size, const int32_t* block_table,
+                               int64_t bt_stride, int32_t max_blocks_per_seq,
+                               const int32_t* context_lens, const int32_t* cu_seqlens_k,
+                               const int32_t* cu_seqlens_q, int32_t max_qlen,
+                               int64_t total_q, int32_t num_seqs, int32_t num_q_heads,
+                               int32_t num_kv_heads, int32_t head_dim, float scale,
+                               int32_t dtype, void* out, int64_t out_stride_tok,
+                               int64_t out_stride_head, void* workspace,
+                               size_t workspace_bytes, int32_t num_splits, void* stream);
+
+/*
+ * Read-only floor of the main kernel: same arguments and grid as
+ * sd_paged_attention_partial, issuing exactly its K/V and q loads (same runs,
+ * order and prefetch) with no math; nothing is written to `out`, and the
+ * workspace is used only as a never-taken sink that keeps the loads. Its time
+ * is the access pattern's own, the floor the main kernel can approach.
+ * Measurement twin of `paged_decode_readonly_kernel` / `read_only`
+ * (nanovllm/kernels/paged_decode_attn_cuda.cu:654-705,1244-1281).
+ */
+int sd_paged_attention_floor(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                             const void* k_cache, const void* v_cache,
+                             int64_t cache_stride_block, int64_t cache_stride_pos,
+                             int64_t cache_stride_head, int64_t num_blocks, int32_t block_size,
+                             const int32_t* block_table, int64_t bt_stride,
+                             int32_t max_blocks_per_seq, const int32_t* context_lens,
+                             const int32_t* cu_seqlens_k, const int32_t* cu_seqlens_q,
+                             int32_t max_qlen, int64_t total_q, int32_t num_seqs,
+                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                             float scale, int32_t dtype, void* out, int64_t out_stride_tok,
+                             int64_t out_stride_head, void* workspace, size_t workspace_bytes,
+                             int32_t num_splits, void* stream);
+
+/*
  * store_kvcache + paged attention in one launch: the decode / verify layer call
  * `Attention.forward` (nanovllm/layers/attention.py:59-82: store_kvcache of the
  * new rows, then flash_attn_with_kvcache or the paged flash_attn_varlen_func).

@@ -111,6 +111,8 @@ SIGNATURES.update({
         _p, _sz, _p]),                  # workspace, bytes, stream
 })
 SIGNATURES["sd_paged_attention_partial"] = SIGNATURES["sd_paged_attention"]
+SIGNATURES["sd_paged_attention_combine"] = SIGNATURES["sd_paged_attention"]
+SIGNATURES["sd_paged_attention_floor"] = SIGNATURES["sd_paged_attention"]
 # sd_paged_attention without (workspace, workspace_bytes): the static-scratch form
 _attn_args = SIGNATURES["sd_paged_attention"][1]
 SIGNATURES["sd_paged_attention_noalloc"] = (ctypes.c_int, _attn_args[:-4] + _attn_args[-2:])

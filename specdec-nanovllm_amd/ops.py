@@ -81,6 +81,19 @@ def _cache_geometry(k_cache: torch.Tensor, layout: str):
     return num_blocks, block_size, num_kv_heads, head_dim, sb, sp, sh
 
 
+def paged_attention_workspace_bytes(num_seqs: int, max_seqlen_q: int, num_q_heads: int,
+                                    num_kv_heads: int, max_ctx: int, num_splits: int = 0,
+                                    device: torch.device | str | None = None) -> int:
+    """Bytes of the split-KV workspace ``paged_attention`` uses for these sizes on
+    ``device`` (the plan follows the device's compute units)."""
+    lib = _lib.load()
+    with torch.cuda.device(torch.device(device) if device is not None else
+                           torch.cuda.current_device()):
+        return int(lib.sd_paged_attention_workspace_size(
+            int(num_seqs), int(max_seqlen_q), int(num_q_heads), int(num_kv_heads), 128,
+            int(max_ctx), int(num_splits)))
+
+
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                     block_table: torch.Tensor, scale: float, *,
                     context_lens: torch.Tensor | None = None,
@@ -90,14 +103,20 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
                     out: torch.Tensor | None = None, main_only: bool = False,
                     key: torch.Tensor | None = None, value: torch.Tensor | None = None,
                     slot_mapping: torch.Tensor | None = None,
-                    no_alloc: bool = False) -> torch.Tensor:
+                    no_alloc: bool = False, twin: str | None = None,
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Paged decode (``cu_seqlens_q is None``: one query row per sequence) or
     speculative-verify attention (rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]``,
     bottom-right causal), GQA, split-KV.
 
     q: (total_q, num_q_heads, head_dim); keys per sequence from ``context_lens``
     (B,) or ``cu_seqlens_k`` (B+1,). Returns ``out`` (same shape/dtype as q).
-    ``main_only`` runs only the split-KV main kernel (measurement twin).
+    ``main_only`` runs only the split-KV main kernel (measurement twin; the
+    same as ``twin="main"``). The other measurement twins: ``twin="combine"``
+    runs only the merge over ``workspace`` as a ``twin="main"`` call with the
+    same arguments left it; ``twin="floor"`` issues only the main kernel's loads
+    (no math, ``out`` untouched). ``workspace`` (uint8, at least the size the
+    library asks for) replaces the workspace otherwise allocated per call.
 
     ``key``/``value`` (total_q, num_kv_heads, head_dim) with ``slot_mapping``
     (total_q,): store_kvcache of these rows fused into the same launch — the
@@ -141,10 +160,15 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         out = torch.empty_like(q)
     else:
         assert out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
+    if main_only:
+        twin = "main"
+    if twin not in (None, "main", "combine", "floor"):
+        raise ValueError(f"unknown twin: {twin}")
     fused = key is not None
-    assert not (no_alloc and (fused or main_only)), "no_alloc is the plain attention call"
+    assert not (no_alloc and (fused or twin)), "no_alloc is the plain attention call"
+    assert not (fused and twin), "the measurement twins are plain attention calls"
     if fused:
-        assert value is not None and slot_mapping is not None and not main_only
+        assert value is not None and slot_mapping is not None
         assert key.shape == (total_q, num_kv_heads, head_dim) and value.shape == key.shape
         assert key.dtype == value.dtype == q.dtype
         assert key.stride(-1) == 1 and value.stride(-1) == 1
@@ -154,7 +178,9 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         return out  # (num_seqs == 0 with new rows: the library only stores them)
     lib = _lib.load()
     max_blocks = bt.shape[1]
-    fn = lib.sd_paged_attention_partial if main_only else lib.sd_paged_attention
+    fn = {None: lib.sd_paged_attention, "main": lib.sd_paged_attention_partial,
+          "combine": lib.sd_paged_attention_combine,
+          "floor": lib.sd_paged_attention_floor}[twin]
     new_rows = ()
     if fused:
         slots = _i32(slot_mapping.reshape(-1))
@@ -179,7 +205,14 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         ws_bytes = lib.sd_paged_attention_workspace_size(
             num_seqs, int(max_seqlen_q), num_q_heads, num_kv_heads, head_dim,
             max_blocks * block_size, int(num_splits))
-        ws = _workspace(ws_bytes, dev)
+        if workspace is not None:
+            assert workspace.dtype == torch.uint8 and workspace.is_contiguous()
+            if workspace.numel() < ws_bytes:
+                raise RuntimeError(f"workspace of {workspace.numel()} bytes, {ws_bytes} needed")
+            _lib.require_device(workspace)
+            ws, ws_bytes = workspace, workspace.numel()
+        else:
+            ws = _workspace(ws_bytes, dev)
         rc = fn(*new_rows, q.data_ptr(), q.stride(0), q.stride(1),
                 k_cache.data_ptr(), v_cache.data_ptr(), sb, sp, sh, num_blocks,
                 block_size, bt.data_ptr(), bt.stride(0), max_blocks,

@@ -476,3 +476,43 @@ def test_errors_match_reference_kinds():
         run_decode(q64, k64, v64, bt64, l64)
     with pytest.raises(RuntimeError):  # CPU tensors: no fallback
         ops.paged_attention(q.cpu(), kc.cpu(), vc.cpu(), bt, 0.1, context_lens=lens)
+
+
+# -------------------------------------------------------------- measurement twins
+@pytest.mark.parametrize("bs", [256, 16])
+def test_twins_main_then_combine_is_the_full_call(bs):
+    """The main-only and combine-only twins over one workspace give the full
+    call's output bit for bit; the read-only floor leaves ``out`` untouched."""
+    q, kc, vc, bt, lens = random_case([700, 1, 2049, 4096, 0, 333, 1800, 64], bs=bs, seed=21)
+    print(f"twins: decode 8 seqs, page {bs}", flush=True)
+    full = run_decode(q, kc, vc, bt, lens)
+    nbytes = ops.paged_attention_workspace_bytes(len(lens), 1, q.shape[1], kc.shape[2],
+                                                 bt.shape[1] * bs, device=DEV)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    out = torch.full_like(q, float("nan"))
+    run_decode(q, kc, vc, bt, lens, twin="main", workspace=ws, out=out)
+    run_decode(q, kc, vc, bt, lens, twin="combine", workspace=ws, out=out)
+    assert torch.equal(out.view(torch.int16), full.view(torch.int16))
+    untouched = torch.full_like(q, float("nan"))
+    run_decode(q, kc, vc, bt, lens, twin="floor", workspace=ws, out=untouched)
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(untouched.float()).all())
+
+
+def test_twins_verify_rows():
+    c = workloads.verify_case(8, 6, seed=5)
+    print(f"twins: C3 verify seed {c['seed_used']}", flush=True)
+    kw = dict(cu_seqlens_k=c["cu_k"].to(DEV), cu_seqlens_q=c["cu_q"].to(DEV), max_seqlen_q=7)
+    bt = c["table"].to(DEV)
+    full = ops.paged_attention(c["q"], c["k_cache"], c["v_cache"], bt, c["scale"], **kw)
+    nbytes = ops.paged_attention_workspace_bytes(8, 7, 32, 8, bt.shape[1] * 256, device=DEV)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    out = torch.full_like(c["q"], float("nan"))
+    for twin in ("main", "combine"):
+        ops.paged_attention(c["q"], c["k_cache"], c["v_cache"], bt, c["scale"], twin=twin,
+                            workspace=ws, out=out, **kw)
+    assert torch.equal(out.view(torch.int16), full.view(torch.int16))
+    ops.paged_attention(c["q"], c["k_cache"], c["v_cache"], bt, c["scale"], twin="floor",
+                        workspace=ws, out=full, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), full.view(torch.int16))  # floor wrote nothing
