@@ -211,6 +211,92 @@ __device__ void locate(const AttnParams& p, int s, int& b_out, int& first_out) {
   first_out = run;
 }
 
+// Up to 64 sequences in one pass (lane i holds sequence i): its keys, query
+// rows and first query row are loaded once, and everything the prologues need
+// comes from shuffles of these registers — one round of global loads instead
+// of one per scan.
+struct LaneSeq {
+  int L;     // keys (clamped)
+  int nq;    // query rows
+  int q0;    // first query row
+  int walk;  // keys the main kernel walks
+  int n;     // columns
+  int incl;  // columns of sequences [0, lane] (inclusive scan)
+};
+
+template <bool STORE>
+__device__ __forceinline__ LaneSeq lane_seq(const AttnParams& p) {
+  const int lane = threadIdx.x & 63;
+  LaneSeq ls;
+  ls.L = 0;
+  ls.nq = 1;
+  ls.q0 = lane;
+  const bool in = lane < p.num_seqs;
+  if (in) {
+    const int L = p.ctx ? p.ctx[lane] : (p.cu_k[lane + 1] - p.cu_k[lane]);
+    ls.L = min(max(L, 0), p.max_ctx);
+    if (p.cu_q) {
+      const int a = p.cu_q[lane], c = p.cu_q[lane + 1];
+      ls.q0 = a;
+      ls.nq = min(max(c - a, 0), p.max_qlen);
+    }
+  }
+  ls.walk = STORE ? max(ls.L - ls.nq, 0) : ls.L;
+  ls.n = in ? steps_of(p, ls.walk) : 0;
+  int incl = ls.n;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
+  }
+  ls.incl = incl;
+  return ls;
+}
+
+// SeqInfo of sequence `src` (wave-uniform) from a lane_seq pass; the fields
+// are wave-uniform, so they are moved to scalar registers (control flow on
+// them stays uniform).
+__device__ __forceinline__ SeqInfo seq_info_of(const AttnParams& p, const LaneSeq& ls, int src) {
+  SeqInfo si;
+  si.L = __builtin_amdgcn_readfirstlane(__shfl(ls.walk, src));
+  si.nq = __builtin_amdgcn_readfirstlane(__shfl(ls.nq, src));
+  si.q0 = __builtin_amdgcn_readfirstlane(__shfl(ls.q0, src));
+  si.causal = __builtin_amdgcn_readfirstlane(__shfl(ls.L, src)) - si.nq;
+  si.R = p.G * si.nq;
+  return si;
+}
+
+// Start of workgroup run `run`: total columns, columns per run S, the run's
+// first column s0, the sequence b holding it, b's first column and b's
+// SeqInfo. False when the run has no columns.
+template <bool STORE>
+__device__ __forceinline__ bool run_start(const AttnParams& p, int run, int& total, int& S,
+                                          int& s0, int& b, int& first, SeqInfo& si) {
+  if (p.num_seqs <= 64) {
+    const int lane = threadIdx.x & 63;
+    const LaneSeq ls = lane_seq<STORE>(p);
+    total = __builtin_amdgcn_readfirstlane(__shfl(ls.incl, 63));
+    S = max((total + p.runs - 1) / p.runs, p.min_steps);
+    s0 = run * S;
+    if (s0 >= total) return false;
+    const int excl = ls.incl - ls.n;
+    const unsigned long long hit = __ballot(ls.n > 0 && excl <= s0 && s0 < ls.incl);
+    b = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+    first = __shfl(excl, b);
+    si = seq_info_of(p, ls, b);
+    (void)lane;
+    return true;
+  }
+  total = __builtin_amdgcn_readfirstlane(cols_before<STORE>(p, p.num_seqs));
+  S = max((total + p.runs - 1) / p.runs, p.min_steps);
+  s0 = run * S;
+  if (s0 >= total) return false;
+  locate<STORE>(p, s0, b, first);
+  b = __builtin_amdgcn_readfirstlane(b);
+  si = seq_info<STORE>(p, b);
+  return true;
+}
+
 // Fused store: the 16-byte pieces of the new K and V rows, copied to their
 // slots bit for bit (slot -1 or outside the pool: skipped), as store_kvcache
 // does. The main kernel reads only cached keys, so the combine kernel, which
@@ -320,17 +406,12 @@ void paged_attn_main(AttnParams p) {
   const int h = static_cast<int>(blockIdx.x) % groups * HPW + wave / KS;
   const int ks = wave % KS;  // this wave's 32-key half of a column (KS = 2)
   const int run = static_cast<int>(blockIdx.x) / groups;
-  const int total = __builtin_amdgcn_readfirstlane(cols_before<STORE>(p, p.num_seqs));
-  const int S = max((total + p.runs - 1) / p.runs, p.min_steps);
-  const int s0 = run * S;
-  if (s0 >= total) return;
+  int total, S, s0, b, first;
+  SeqInfo si;
+  if (!run_start<STORE>(p, run, total, S, s0, b, first, si)) return;
   const int s1 = min(s0 + S, total);
-  int b, first;
-  locate<STORE>(p, s0, b, first);
   b = __builtin_amdgcn_readfirstlane(b);
   first = __builtin_amdgcn_readfirstlane(first);
-
-  SeqInfo si = seq_info<STORE>(p, b);
   int n = steps_of(p, si.L);  // columns of sequence b
   int j = s0 - first;
   int j_first = j;  // column at which this workgroup entered the current pair
@@ -578,9 +659,10 @@ void paged_attn_main(AttnParams p) {
   };
 
   // ---- walk [s0, s1): load step s + 1 while computing step s
-  begin_pair();
+  // the first K/V loads go out before the query rows (needed only at compute)
   StepRegs ra, rb;
   load_step(ra, b, h, j, si.L, true);
+  begin_pair();
   int s = s0;
   auto advance = [&](StepRegs& cur, StepRegs& nxt) -> bool {
     // position of step s + 1
@@ -675,7 +757,18 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   __shared__ __attribute__((aligned(16))) float4 s_o[kGroups][32];
   __shared__ float2 s_ml[kGroups];
   const int h = blockIdx.y, b = blockIdx.z;
-  const SeqInfo si = seq_info<STORE>(p, b);
+  // pair b's SeqInfo, its first column f and all columns: one round of loads
+  SeqInfo si;
+  int f, total;
+  if (p.num_seqs <= 64) {
+    const LaneSeq ls = lane_seq<STORE>(p);
+    si = seq_info_of(p, ls, b);
+    total = __shfl(ls.incl, 63);
+    f = __shfl(ls.incl - ls.n, b);
+  } else {
+    si = seq_info<STORE>(p, b);
+    cols_split<STORE>(p, b, f, total);
+  }
   const int grp = threadIdx.x >> 5, d4 = (threadIdx.x & 31) * 4;
   const int rpw = p.comb_rows, nsl = kGroups / rpw;
   const int sl = grp / rpw;
@@ -703,8 +796,6 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
     }
   }
 
-  int f, total;
-  cols_split<STORE>(p, b, f, total);
   float M = -INFINITY, l = 0.f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
   bool final_by_main = !STORE && n == 0;  // (zeros written below)
