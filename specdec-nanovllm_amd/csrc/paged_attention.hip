@@ -363,17 +363,28 @@ __device__ __forceinline__ void store4(uint16_t* dst, f32x4 v, float s) {
   *reinterpret_cast<uint2*>(dst) = w;
 }
 
-// LDS of the main kernel: one K and one V tile per wave.
+// Bytes of one K + V tile of 32 keys (padded pitches).
+constexpr int kTileBytes = kStep * (kKPitch + kVPitch) * 2;
+
+// LDS of the main kernel: one K and one V tile per wave (TS = 1), or two
+// (double-buffered) shared tiles per pair of waves (TS = 2): NW tiles either way.
 template <int NW>
-constexpr int smem_bytes() { return NW * kStep * (kKPitch + kVPitch) * 2; }
+constexpr int smem_bytes() { return NW * kTileBytes; }
 
 // One wave's share of one workgroup step: 32 keys of K and of V, lane l
 // holding key 4 r + l/16, dims 8 (l%16) .. +8 of k[r] / v[r] — 16 lanes read one
 // whole 256-byte row, so every load instruction moves four full rows. Both
-// tiles are then transposed through LDS into MFMA operand order.
-struct StepRegs {
+// tiles are then transposed through LDS into MFMA operand order. With TS = 2
+// a wave loads one of the two tensors (d: K for its pair's first wave, V for
+// the second), in the same lane layout.
+template <int TS>
+struct StepRegsT {
   u32x4 k[8];
   u32x4 v[8];
+};
+template <>
+struct StepRegsT<2> {
+  u32x4 d[8];
 };
 
 // ONE_PAGE: block_size % 32 == 0, so a wave's 32-key slice never crosses a
@@ -390,9 +401,19 @@ constexpr int main_occupancy() { return RT == 1 ? 2 : 1; }
 // FLOOR: the measurement twin that issues exactly the loads of the kernel
 // (same grid, runs, order and prefetch) with no math and no output — the
 // access pattern's own time.
-template <typename T, int RT, bool ONE_PAGE, bool STORE, int NW, int KS = 1, bool FLOOR = false>
+// TS = 2 (tile split, verify's 2 row tiles): two waves share each 32-key step
+// of a kv head and take one 16-row tile each (RT = 1 per wave). The first
+// loads the step's K rows, the second its V rows; both write them into their
+// pair's double-buffered LDS tile, meet at a workgroup barrier, and compute
+// their own tile from the shared K and V. A wave then holds half the
+// accumulator and half the prefetch of a two-tile wave, so the kernel runs at
+// two waves per SIMD without spilling.
+template <typename T, int RT, bool ONE_PAGE, bool STORE, int NW, int KS = 1, bool FLOOR = false,
+          int TS = 1>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(main_occupancy<RT>())))
 void paged_attn_main(AttnParams p) {
+  static_assert(TS == 1 || RT == 1, "a tile-split wave holds one row tile");
+  using StepRegs = StepRegsT<TS>;
   __shared__ __attribute__((aligned(16))) char smem[smem_bytes<NW>()];
 
   const int tid = threadIdx.x;
@@ -401,10 +422,12 @@ void paged_attn_main(AttnParams p) {
   const int lr = lane & 15, lg = lane >> 4;
 
   // ---- this wave's kv head and the workgroup's run of columns [s0, s1)
-  constexpr int HPW = NW / KS;  // kv heads per workgroup
+  constexpr int HPW = NW / (KS * TS);  // kv heads per workgroup
   const int groups = p.Hkv / HPW;
-  const int h = static_cast<int>(blockIdx.x) % groups * HPW + wave / KS;
-  const int ks = wave % KS;  // this wave's 32-key half of a column (KS = 2)
+  const int h = static_cast<int>(blockIdx.x) % groups * HPW + wave / (KS * TS);
+  const int ks = wave / TS % KS;  // this wave's 32-key half of a column (KS = 2)
+  const int ts = wave % TS;       // TS = 2: this wave's row tile and loaded tensor
+  const int tile0 = TS == 2 ? ts : 0;
   const int run = static_cast<int>(blockIdx.x) / groups;
   int total, S, s0, b, first;
   SeqInfo si;
@@ -425,7 +448,7 @@ void paged_attn_main(AttnParams p) {
   auto begin_pair = [&]() {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const int row = rt * 16 + lr;
+      const int row = (tile0 + rt) * 16 + lr;
       const int qi = row / p.G, g = row - qi * p.G;
       const int64_t qt = si.q0 + qi;
       const bool valid = row < si.R && qt >= 0 && qt < p.total_q;
@@ -468,39 +491,66 @@ void paged_attn_main(AttnParams p) {
         const int tok = min(t0 + r * 4 + lg, last);
         const uint32_t off =  // bytes
             used ? (static_cast<uint32_t>(tok - t0) * p.c_spos32 + lr * 8) * 2u : 0u;
-        R.k[r] = sd::load16_stream(kpg + off);
-        R.v[r] = sd::load16_stream(vpg + off);
+        if constexpr (TS == 2) {
+          R.d[r] = sd::load16_stream((ts == 0 ? kpg : vpg) + off);
+        } else {
+          R.k[r] = sd::load16_stream(kpg + off);
+          R.v[r] = sd::load16_stream(vpg + off);
+        }
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         const int tok = min(t0 + r * 4 + lg, last);
         const int64_t off = used ? kv_row(p, btrow, tok) + hoff + lr * 8 : 0;
-        R.k[r] = sd::load16_stream(p.kc + off);
-        R.v[r] = sd::load16_stream(p.vc + off);
+        if constexpr (TS == 2) {
+          R.d[r] = sd::load16_stream((ts == 0 ? p.kc : p.vc) + off);
+        } else {
+          R.k[r] = sd::load16_stream(p.kc + off);
+          R.v[r] = sd::load16_stream(p.vc + off);
+        }
       }
     }
   };
 
-  uint16_t* kl = reinterpret_cast<uint16_t*>(smem) + wave * (kStep * (kKPitch + kVPitch));
+  // TS = 1: this wave's own tile. TS = 2: its pair's two tiles (step parity).
+  char* const tiles = smem + (TS == 2 ? (wave / 2) * 2 : wave) * kTileBytes;
+  uint16_t* kl = reinterpret_cast<uint16_t*>(tiles);
   uint16_t* vl = kl + kStep * kKPitch;
   u32x4 fold = {0u, 0u, 0u, 0u};  // FLOOR: every loaded word is consumed here
 
-  auto compute_step = [&](StepRegs& R, int cj) {
+  auto compute_step = [&](StepRegs& R, int cj, int par) {
     const int tb = cj * p.col_keys + ks * kStep;
-    if (tb >= si.L) return;  // wave-uniform (KS = 2: the last half of a column may be empty)
     if constexpr (FLOOR) {
+      if (tb >= si.L) return;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) fold ^= R.k[r] ^ R.v[r];
+      for (int r = 0; r < 8; ++r) {
+        if constexpr (TS == 2) fold ^= R.d[r];
+        else fold ^= R.k[r] ^ R.v[r];
+      }
       return;
     }
-    // ---- stage the 32 K and V rows of this step (row-major, padded pitch)
+    if constexpr (TS == 2) {
+      // ---- this wave's tensor of the step into the pair's tile `par`; both
+      //      waves of every pair reach the barrier on every step
+      kl = reinterpret_cast<uint16_t*>(tiles + par * kTileBytes);
+      vl = kl + kStep * kKPitch;
+      uint16_t* dst = ts == 0 ? kl : vl;
+      const int pitch = ts == 0 ? kKPitch : kVPitch;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      sd::store16(kl + (r * 4 + lg) * kKPitch + lr * 8, R.k[r]);
-      sd::store16(vl + (r * 4 + lg) * kVPitch + lr * 8, R.v[r]);
+      for (int r = 0; r < 8; ++r) sd::store16(dst + (r * 4 + lg) * pitch + lr * 8, R.d[r]);
+      __syncthreads();
+      if (tb >= si.L) return;  // wave-uniform (KS = 2: the last half may be empty)
+    } else {
+      if (tb >= si.L) return;  // wave-uniform (KS = 2: the last half of a column may be empty)
+      // ---- stage the 32 K and V rows of this step (row-major, padded pitch)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        sd::store16(kl + (r * 4 + lg) * kKPitch + lr * 8, R.k[r]);
+        sd::store16(vl + (r * 4 + lg) * kVPitch + lr * 8, R.v[r]);
+      }
+      sd::wave_lds_sync();  // rows written by other lanes of this wave are read below
     }
-    sd::wave_lds_sync();  // rows written by other lanes of this wave are read below
     // ---- S^T tiles: lane holds S[row lr][key tb + 16 tt + 4 lg + i]; the K
     //      A operand of MFMA s is key 16 tt + lr, dims 32 s + 8 lg .. +8
     f32x4 sc[RT][2];
@@ -586,7 +636,9 @@ void paged_attn_main(AttnParams p) {
         acc[rt][dt] = sd::Elem<T>::mfma(vop, plo[rt], acc[rt][dt]);
       }
     }
-    sd::wave_lds_sync();  // every lane has read the tile before the next step overwrites it
+    // every lane has read the tile before the next step overwrites it (TS = 2:
+    // the next step writes the other tile, and the barrier orders the one after)
+    if constexpr (TS == 1) sd::wave_lds_sync();
   };
 
   // Write this wave's state of the current pair from registers: normalised
@@ -600,12 +652,17 @@ void paged_attn_main(AttnParams p) {
     for (int rt = 0; rt < RT; ++rt) lsum[rt] = sd::sum_over_groups(l_run[rt]);
     if constexpr (KS == 2) {
       // the second wave of a head hands (m, l, acc) to the first through its
-      // own (idle) K/V tile: rows of kD + 4 floats
+      // own (idle) K/V tile: rows of kD + 4 floats (TS = 2: the second key
+      // half's pair of tiles, one state block per row tile)
       constexpr int kPitch = kD + 4;
-      static_assert(RT * 16 * kPitch * 4 <= kStep * (kKPitch + kVPitch) * 2, "state fits the tile");
+      static_assert(RT * 16 * kPitch * 4 <= kTileBytes, "state fits the tile");
       __syncthreads();  // every wave is done with its tiles
+      float* const xchg = TS == 2
+          ? reinterpret_cast<float*>(smem + ((wave / (KS * TS)) * KS * TS + TS) * kTileBytes) +
+                ts * 16 * kPitch
+          : nullptr;
       if (ks == 1) {
-        float* xs = reinterpret_cast<float*>(kl);
+        float* xs = TS == 2 ? xchg : reinterpret_cast<float*>(kl);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           float* xr = xs + (rt * 16 + lr) * kPitch;
@@ -617,7 +674,8 @@ void paged_attn_main(AttnParams p) {
       }
       __syncthreads();
       if (ks == 0) {
-        const float* ys = reinterpret_cast<const float*>(kl + kStep * (kKPitch + kVPitch));
+        const float* ys = TS == 2 ? xchg
+                                  : reinterpret_cast<const float*>(kl + kStep * (kKPitch + kVPitch));
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           const float* yr = ys + (rt * 16 + lr) * kPitch;
@@ -638,7 +696,7 @@ void paged_attn_main(AttnParams p) {
     for (int rt = 0; rt < RT; ++rt) {
       if (KS == 2 && ks != 0) break;
       const float l = lsum[rt];
-      const int row = rt * 16 + lr;
+      const int row = (tile0 + rt) * 16 + lr;
       const int qi = row / p.G, g = row - qi * p.G;
       const int64_t qt = si.q0 + qi;
       if (row >= si.R || qt < 0 || qt >= p.total_q) continue;
@@ -679,7 +737,7 @@ void paged_attn_main(AttnParams p) {
     // the last step issues a dummy prefetch so that every iteration issues the
     // same loads
     load_step(nxt, more ? nb : b, h, more ? nj : j, more ? nL : si.L, more);
-    compute_step(cur, j);
+    compute_step(cur, j, s & 1);
     const bool pair_end = j + 1 == n;
     // STORE: partials only; the combine adds the new rows' keys
     if (pair_end || !more) flush(!STORE && pair_end && j_first == 0);
@@ -935,6 +993,7 @@ __global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
 // ------------------------------------------------------------------ host
 struct Plan {
   int RT;         // 16-row tiles of query rows
+  int TS;         // 2: the row tiles on two waves that share each step's K/V
   int KS;         // waves per kv head (two 32-key halves of a column when 2)
   int NW;         // waves per main workgroup
   int runs;
@@ -954,20 +1013,24 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   const int G = Hq / Hkv;
   pl.rmax = G * max_qlen;
   pl.RT = pl.rmax <= 16 ? 1 : 2;
+  // two row tiles: one per wave, two waves sharing each step's loads
+  pl.TS = pl.RT == 2 ? 2 : 1;
   // two waves per kv head, half the runs and partials: two row tiles (verify),
   // and small batches, whose pairs each collect a partial from many runs
   pl.KS = (pl.RT == 2 || num_seqs <= 4) && Hkv % 2 == 0 ? 2 : 1;
-  pl.NW = pl.KS == 2 ? 4 : (Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1));
+  pl.NW = pl.TS == 2 ? 2 * pl.KS : (pl.KS == 2 ? 4 : (Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1)));
   int64_t runs;
   if (num_splits > 0) {
     runs = static_cast<int64_t>(num_splits) * num_seqs;
     pl.min_steps = 1;
   } else {
-    const int occ = pl.RT == 1 ? main_occupancy<1>() : main_occupancy<2>();
-    runs = static_cast<int64_t>(sd::device_cus()) * 4 * occ / (Hkv * pl.KS);
-    pl.min_steps = pl.RT == 1 || pl.KS == 2 ? 1 : 2;  // at least 64 keys per run with two tiles
+    // waves per SIMD of the instance that runs (a tile-split wave holds one tile)
+    const int occ = pl.RT == 1 || pl.TS == 2 ? main_occupancy<1>() : main_occupancy<2>();
+    runs = static_cast<int64_t>(sd::device_cus()) * 4 * occ / (Hkv * pl.KS * pl.TS);
+    // at least 64 keys per run with two tiles on one wave
+    pl.min_steps = pl.RT == 1 || pl.KS == 2 || pl.TS == 2 ? 1 : 2;
   }
-  const int groups = Hkv / (pl.NW / pl.KS);
+  const int groups = Hkv / (pl.NW / (pl.KS * pl.TS));
   const int64_t cap = (1 << 20) / groups > 1 ? (1 << 20) / groups : 1;  // grid of at most 2^20
   runs = runs < 1 ? 1 : (runs > cap ? cap : runs);
   pl.runs = static_cast<int>(runs);
@@ -984,22 +1047,27 @@ size_t ws_bytes(const Plan& pl) {
   return ml_bytes(pl) + static_cast<size_t>(pl.slots) * pl.rmax * kD * sizeof(float);
 }
 
-template <typename T, int RT, bool STORE, int NW, int KS = 1, bool FLOOR = false>
+template <typename T, int RT, bool STORE, int NW, int KS = 1, bool FLOOR = false, int TS = 1>
 void launch_main(const AttnParams& p, hipStream_t st) {
   if (p.block_size % kStep == 0)
-    hipLaunchKernelGGL((paged_attn_main<T, RT, true, STORE, NW, KS, FLOOR>), dim3(p.nwg),
+    hipLaunchKernelGGL((paged_attn_main<T, RT, true, STORE, NW, KS, FLOOR, TS>), dim3(p.nwg),
                        dim3(NW * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((paged_attn_main<T, RT, false, STORE, NW, KS, FLOOR>), dim3(p.nwg),
+    hipLaunchKernelGGL((paged_attn_main<T, RT, false, STORE, NW, KS, FLOOR, TS>), dim3(p.nwg),
                        dim3(NW * 64), 0, st, p);
 }
 
 template <typename T, int RT, bool STORE, bool FLOOR = false>
 void launch_main(const AttnParams& p, const Plan& pl, hipStream_t st) {
-  if (pl.KS == 2) return launch_main<T, RT, STORE, 4, 2, FLOOR>(p, st);
-  if (pl.NW == 4) launch_main<T, RT, STORE, 4, 1, FLOOR>(p, st);
-  else if (pl.NW == 2) launch_main<T, RT, STORE, 2, 1, FLOOR>(p, st);
-  else launch_main<T, RT, STORE, 1, 1, FLOOR>(p, st);
+  if constexpr (RT == 2) {  // two row tiles, one per wave (RT = 1 per wave, TS = 2)
+    if (pl.KS == 2) launch_main<T, 1, STORE, 4, 2, FLOOR, 2>(p, st);
+    else launch_main<T, 1, STORE, 2, 1, FLOOR, 2>(p, st);
+  } else {
+    if (pl.KS == 2) launch_main<T, RT, STORE, 4, 2, FLOOR>(p, st);
+    else if (pl.NW == 4) launch_main<T, RT, STORE, 4, 1, FLOOR>(p, st);
+    else if (pl.NW == 2) launch_main<T, RT, STORE, 2, 1, FLOOR>(p, st);
+    else launch_main<T, RT, STORE, 1, 1, FLOOR>(p, st);
+  }
 }
 
 template <typename T, int RT>
