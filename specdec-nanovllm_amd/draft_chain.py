@@ -6,7 +6,12 @@ q/k RMSNorm, rotate-half RoPE with theta 1e6 — nanovllm/models/qwen3.py:14-216
 layers/layernorm.py, layers/rotary_embedding.py). Every linear (qkv, o, gate_up,
 down and lm_head) is W8A16 per-channel int8, quantized once at construction
 with ``layers.quant.quantize_weight``; the KV cache is bf16, paged in 256-token
-blocks, filled with a synthetic (random) ``ctx_len``-token context per sequence.
+blocks. Its ``ctx_len``-token context per sequence is prefilled from uniform
+random token ids (``context="prefill"``): the same decoder stack runs over the
+ids at positions 0 .. ctx_len-1 (the linears on the dequantized weights in
+bf16, attention on this library's varlen causal prefill kernel) and its k / v
+rows are written to the pages; ``context="randn"`` fills the pages with N(0,1)
+values instead.
 
 One draft step is the reference's batched single-token forward
 (nanovllm/spec_decode/draft_proposer.py:493-510, :527-550): per sequence the
@@ -15,8 +20,11 @@ the key count ``pos + 1``; the layers call ``store_kvcache``, paged decode
 attention and the W8A16 linears of this library, and the next token is the
 argmax of the logits (the greedy draft). The hot-path ops run on the gfx950
 kernels. The neighbours of the path — RMSNorm (+ residual add), q/k norm +
-RoPE, SiLU*mul and the argmax — are plain eager torch (no torch.compile) with
-``fused=False``, or this library's fused neighbour kernels with ``fused=True``:
+RoPE and SiLU*mul — are plain eager torch (no torch.compile) with
+``fused=False`` (the greedy argmax is this library's sampler in both forms:
+torch's argmax over a 151936-wide row clears its reduction semaphores with a
+memset, which a captured graph does not replay reliably), or this library's
+fused neighbour kernels with ``fused=True``:
 add + RMSNorm inside the projection that consumes it (qkv, gate_up, lm_head;
 at up to 4 rows, two launches beyond), q/k norm + RoPE + store_kvcache in one
 launch on the qkv output (the attention reads q through strides), SiLU*mul
@@ -46,7 +54,8 @@ class DraftChain:
                  hidden: int = 1024, heads: int = 16, kv_heads: int = 8, head_dim: int = 128,
                  inter: int = 3072, vocab: int = 151936, theta: float = 1e6, eps: float = 1e-6,
                  block_size: int = 256, seed: int = 0, device="cuda",
-                 dtype: torch.dtype = torch.bfloat16, fused: bool = False):
+                 dtype: torch.dtype = torch.bfloat16, fused: bool = False,
+                 context: str = "prefill"):
         self.B, self.ctx_len, self.k = batch, ctx_len, k
         self.fused = fused
         self.L, self.H, self.Hq, self.Hkv, self.D = layers, hidden, heads, kv_heads, head_dim
@@ -87,11 +96,20 @@ class DraftChain:
         # context of ctx_len rows per sequence; pages are a seeded shuffle
         self.pages_per_seq = math.ceil((ctx_len + k) / block_size)
         nblk = batch * self.pages_per_seq
-        self.kv = torch.randn((2, layers, nblk, block_size, kv_heads, head_dim), generator=g,
-                              device=self.dev).to(dtype)
+        if context == "randn":
+            self.kv = torch.randn((2, layers, nblk, block_size, kv_heads, head_dim),
+                                  generator=g, device=self.dev).to(dtype)
+        elif context == "prefill":
+            self.kv = torch.zeros((2, layers, nblk, block_size, kv_heads, head_dim),
+                                  device=self.dev, dtype=dtype)
+        else:
+            raise ValueError(f"unknown context: {context}")
         cg = torch.Generator().manual_seed(seed + 1)
         perm = torch.randperm(nblk, generator=cg).to(torch.int32)
         self.block_table = perm.view(batch, self.pages_per_seq).to(self.dev)
+        if context == "prefill":
+            ids = torch.randint(0, vocab, (batch, ctx_len), generator=cg).to(self.dev)
+            self._prefill(ids)
 
         # per-step static metadata: positions, slots, key counts
         bt = perm.view(batch, self.pages_per_seq)
@@ -109,6 +127,49 @@ class DraftChain:
         # residual stream of the fused step: the norm fused into a projection
         # writes x + residual to the buffer the current residual is not in
         self._res = torch.empty((2, batch, hidden), device=self.dev, dtype=dtype)
+
+    # -------------------------------------------------------------------- context
+    @torch.no_grad()
+    def _prefill(self, ids: torch.Tensor) -> None:
+        """Prefill of the context: the decoder stack over ``ids`` (batch,
+        ctx_len) at positions 0 .. ctx_len-1, its k / v rows written to the
+        pages of every layer. Setup, not the measured path: the linears use the
+        dequantized weights in bf16 (torch), attention the varlen causal prefill
+        kernel on contiguous rows, one layer at a time."""
+        B, C, Hq, Hkv, D = self.B, self.ctx_len, self.Hq, self.Hkv, self.D
+        if C == 0:
+            return
+        from .layers.quant import dequantize_weight
+
+        def lin(x, qw):
+            return x @ dequantize_weight(*qw).to(self.dtype).T.contiguous()
+
+        pos = torch.arange(C, device=self.dev).repeat(B)
+        cos, sin = self.cos[pos], self.sin[pos]
+        cu = torch.arange(0, (B + 1) * C, C, dtype=torch.int32, device=self.dev)
+        bt = self.block_table.long()
+        p = torch.arange(C, device=self.dev)
+        slots = (bt[:, p // self.bs] * self.bs + p % self.bs).reshape(-1)  # (B*C,)
+        h = self.embed[ids.reshape(-1)]
+        residual = None
+        for li, lw in enumerate(self.layers):
+            if residual is None:
+                residual = h
+                x = self._rms(h, lw["in_norm"])
+            else:
+                x, residual = self._add_rms(h, residual, lw["in_norm"])
+            q, kk, v = lin(x, lw["qkv"]).split([Hq * D, Hkv * D, Hkv * D], dim=-1)
+            q = self._rope(self._rms(q.reshape(-1, Hq, D), lw["q_norm"]), cos, sin)
+            kk = self._rope(self._rms(kk.reshape(-1, Hkv, D), lw["k_norm"]), cos, sin)
+            v = v.reshape(-1, Hkv, D).contiguous()
+            self.kv[0, li].view(-1, Hkv, D)[slots] = kk
+            self.kv[1, li].view(-1, Hkv, D)[slots] = v
+            o = ops.prefill_attention(q.contiguous(), kk.contiguous(), v, cu, cu, C, self.scale)
+            h = lin(o.reshape(-1, Hq * D), lw["o"])
+            x, residual = self._add_rms(h, residual, lw["post_norm"])
+            gate, up = lin(x, lw["gate_up"]).chunk(2, dim=-1)
+            h = lin(torch.nn.functional.silu(gate) * up, lw["down"])
+            del q, kk, v, o, x, gate, up
 
     # ------------------------------------------------------------------ neighbours
     def _rms(self, x, w):
@@ -160,8 +221,11 @@ class DraftChain:
             h = ops.w8a16_linear(torch.nn.functional.silu(gate) * up, *lw["down"])
         x, _ = self._add_rms(h, residual, self.final_norm)
         logits = ops.w8a16_linear(x, *self.lm_head)
-        nxt = logits.argmax(dim=-1)
-        self.tokens[s + 1].copy_(nxt)
+        # the greedy argmax on this library's sampler (first index among ties,
+        # as torch.argmax): torch's argmax over a vocabulary-wide row is a
+        # multi-block reduction whose semaphores are cleared by a memset, and a
+        # captured memset node is not reliable on graph replay here
+        ops.sample(logits, out=self.tokens[s + 1])
         return logits
 
     def _step_fused(self, s: int) -> torch.Tensor:

@@ -95,13 +95,15 @@ def decode_case(batch: int, *, num_q_heads=32, num_kv_heads=8, head_dim=128, blo
 
 def verify_case(batch: int = 8, k: int = 6, *, num_q_heads=32, num_kv_heads=8, head_dim=128,
                 block_size=256, num_blocks=2048, len_range=(1500, 2600), seed=0,
-                dtype=torch.bfloat16, device="cuda"):
+                dtype=torch.bfloat16, device="cuda", sets: int = 1):
     """C3 speculative-verify inputs: ``k+1`` query rows per sequence at positions
     len-1 .. len+k-1, keys [0, len+k). ``keys`` = len + k per sequence.
 
     The lengths come from the first seed >= ``seed`` for which at least one
     sequence's k+1 rows straddle a page boundary (C3 requires such a row);
-    ``seed_used`` records it."""
+    ``seed_used`` records it. ``sets`` > 1 adds ``tables`` / ``slot_sets``:
+    that many block tables over disjoint pages of the pool (the first is
+    ``table``) with their slots, for timing on pages not yet read."""
     for s in range(seed, seed + 1000):
         g = torch.Generator().manual_seed(s)
         lens = torch.randint(len_range[0], len_range[1] + 1, (batch,), generator=g,
@@ -112,7 +114,8 @@ def verify_case(batch: int = 8, k: int = 6, *, num_q_heads=32, num_kv_heads=8, h
     seed = s
     keys = lens + k
     width = math.ceil((len_range[1] + k) / block_size)
-    bt = block_tables_for(keys.tolist(), block_size, num_blocks, g, width)[0]
+    tables = block_tables_for(keys.tolist(), block_size, num_blocks, g, width, sets)
+    bt = tables[0]
     n = k + 1
     cu_q = torch.arange(0, (batch + 1) * n, n, dtype=torch.int32)
     cu_k = torch.zeros(batch + 1, dtype=torch.int32)
@@ -132,6 +135,8 @@ def verify_case(batch: int = 8, k: int = 6, *, num_q_heads=32, num_kv_heads=8, h
         k_new=_randn((batch * n, num_kv_heads, head_dim), dg, device, dtype),
         v_new=_randn((batch * n, num_kv_heads, head_dim), dg, device, dtype),
         slots=slots_for(bt, positions, block_size),
+        tables=tables,
+        slot_sets=[slots_for(t, positions, block_size) for t in tables],
         scale=head_dim ** -0.5,
     )
 

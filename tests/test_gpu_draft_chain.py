@@ -1,11 +1,15 @@
 """GPU parity of the C5 draft chain (draft_chain.DraftChain) against a plain
 torch float32 restatement of the same decoder step: dequantized weights
 (``q * scale``), softmax attention over the gathered paged rows, the same bf16
-rounding points between ops. Floating point: logits of every step must agree to
+rounding points between ops. Floating point: logits must agree to
 ``max|got - ref| <= 2e-2 * max|ref|`` (bf16 activations between ops), and the
 HIP-graph replay of the chain must reproduce the eager chain bit for bit.
 Both forms of the step are covered: eager-torch neighbours and this library's
-fused neighbour kernels.
+fused neighbour kernels — on a small stack (every step checked), and at the C5
+configuration itself (28 layers, hidden 1024, 16 q / 8 kv heads, intermediate
+3072, vocab 151936, a 2048-token context prefilled from uniform random token
+ids, k = 6 steps, batch 1 and 16: step 0 checked against the reference, every
+drafted token against the argmax of its logits, the graph replay bitwise).
 """
 import pytest
 import torch
@@ -119,3 +123,56 @@ def test_draft_chain_graph_replay_is_bitwise_eager(fused):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(ch.tokens, eager)
+
+
+# ------------------------------------------------------------ the C5 configuration
+@pytest.fixture(scope="module", params=[1, 16], ids=["B1", "B16"])
+def c5_chain(request):
+    B = request.param
+    print(f"C5 chain: building B={B}, 28 layers, ctx 2048 (prefill of random ids)", flush=True)
+    ch = DraftChain(B, ctx_len=2048, k=6, seed=B)
+    torch.cuda.synchronize()
+    yield ch
+    del ch
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["eager", "fused"])
+def test_c5_configuration(c5_chain, fused):
+    ch = c5_chain
+    ch.fused = fused
+    print(f"C5 chain B={ch.B} fused={fused}: eager steps", flush=True)
+    kv0, tok0 = ch.kv.clone(), ch.tokens.clone()
+    logits = [ch.step(s).float() for s in range(ch.k)]
+    torch.cuda.synchronize()
+    eager_tok, eager_kv = ch.tokens.clone(), ch.kv.clone()
+    for s in range(ch.k):  # the greedy draft: each token is the argmax of its own logits
+        assert torch.equal(eager_tok[s + 1], logits[s].argmax(dim=-1)), f"step {s}"
+    print(f"C5 chain B={ch.B} fused={fused}: float32 reference of step 0", flush=True)
+    kv_ref = kv0.clone()
+    ref = ref_step(ch, kv_ref, tok0[0], 0)
+    err = (logits[0] - ref).abs().max().item()
+    assert err <= 2e-2 * ref.abs().max().item(), f"step 0: max err {err:.4g}"
+    del kv_ref, ref, logits
+    print(f"C5 chain B={ch.B} fused={fused}: HIP graph of the 6 steps", flush=True)
+    ch.kv.copy_(kv0)
+    ch.tokens.copy_(tok0)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        ch.chain()
+    torch.cuda.current_stream().wait_stream(st)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ch.chain()
+    for _ in range(2):
+        ch.kv.copy_(kv0)
+        ch.tokens.copy_(tok0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ch.tokens, eager_tok)
+        assert torch.equal(ch.kv.view(torch.int16), eager_kv.view(torch.int16))
+    ch.kv.copy_(kv0)  # the fixture's initial state for the next form
+    ch.tokens.copy_(tok0)
+    del g, kv0, eager_kv
