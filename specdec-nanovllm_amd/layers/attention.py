@@ -9,10 +9,9 @@ the new K/V rows through the slot mapping, then (both in one fused launch)
   sequence over ``context_lens`` keys; the output has flash-attn's
   (B, 1, Hq, D) shape, as at attention.py:77-81;
 * verify / prefix-cache prefill (``block_tables`` set): paged varlen attention
-  with bottom-right causal masking, (total_q, Hq, D).
-
-Plain prefill over contiguous k/v is not on the decode path and raises
-``NotImplementedError``.
+  with bottom-right causal masking, (total_q, Hq, D);
+* plain prefill (contiguous k / v, no block table): the store, then the
+  varlen causal prefill kernel over the contiguous rows.
 """
 from __future__ import annotations
 

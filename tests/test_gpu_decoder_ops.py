@@ -188,10 +188,16 @@ def test_sampled_tokens_match_oracle():
     want = od.sample(logits.numpy(), temps.numpy(), int(state[0]), int(state[1]))
     keys = od.sample_keys(logits.numpy(), np.where(temps.numpy() > 0, temps.numpy(), 1),
                           int(state[0]), int(state[1]))
-    for r in np.nonzero(got != want)[0]:
-        assert temps[r] > 0, f"greedy row {r} differs"
-        assert keys[r, want[r]] - keys[r, got[r]] < 1e-4, f"row {r}: {got[r]} vs {want[r]}"
-    assert (got == want).mean() > 0.9
+    # exact on every row whose two best race keys are further apart than the
+    # key's rounding (the kernel forms keys in the log2 domain with the native
+    # log: a few float32 ulps of |key| <= ~20, far below 1e-3); a measured
+    # near-tie may take either of its tied columns
+    top2 = np.sort(keys, axis=-1)[:, -2:]
+    tie = (top2[:, 1] - top2[:, 0] < 1e-3) & (temps.numpy() > 0)
+    assert np.array_equal(got[~tie], want[~tie]), np.nonzero((got != want) & ~tie)[0]
+    for r in np.nonzero(tie)[0]:
+        assert keys[r, want[r]] - keys[r, got[r]] < 1e-3, f"row {r}: {got[r]} vs {want[r]}"
+    assert tie.sum() <= 2, f"{tie.sum()} near-ties in {rows} rows"
 
 
 def test_sampling_law_on_gpu():

@@ -1,8 +1,8 @@
 """GPU parity of the variable-length causal (prefill) attention kernel
 (csrc/prefill_attention.hip, through the C ABI) against float64 attention on
-the CPU of the same 16-bit inputs: per sequence, softmax(q K^T * scale) V with
-row t seeing keys [0, nk - nq + t] (bottom-right causal, flash-attn varlen
-semantics, nanovllm/layers/attention.py:64-70). Tolerance as for decode:
+the CPU of the same 16-bit inputs (the oracle's ``attend``): per sequence,
+softmax(q K^T * scale) V with row t seeing keys [0, nk - nq + t] (bottom-right
+causal, flash-attn varlen semantics, nanovllm/layers/attention.py:64-70). Tolerance as for decode:
 |o - ref| <= 2e-3 + 1e-2 |ref|. Covers contiguous K/V batches with ragged
 lengths (1 .. 513 rows, tile edges), GQA ratios 1 / 4 / 8, fp16, the
 prefix-cached paged form (nk > nq), the flash_attn_varlen_func dispatch and
@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from conftest import assert_close_attn, to_np
+from oracle import paged_attention as opa
 from specdec_nanovllm_amd import ops, workloads
 from specdec_nanovllm_amd.flash_attn_compat import flash_attn_varlen_func
 from specdec_nanovllm_amd.layers.attention import Attention
@@ -25,23 +26,15 @@ DEV = "cuda"
 
 
 def ref_varlen(q, k, v, cu_q, cu_k, scale):
-    """float64 per-sequence causal attention (bottom-right), k/v (total_k, Hkv, D)."""
-    q, k, v = q.double().cpu(), k.double().cpu(), v.double().cpu()
-    G = q.shape[1] // k.shape[1]
-    out = torch.zeros_like(q)
+    """float64 per-sequence bottom-right causal attention, k/v (total_k, Hkv, D):
+    the pinned oracle's ``attend`` (checked against torch SDPA with
+    causal_lower_right in tests/test_oracle_attention.py) on each sequence."""
+    q, k, v = to_np(q.float()), to_np(k.float()), to_np(v.float())
+    out = np.zeros(q.shape, dtype=np.float64)
     for b in range(len(cu_q) - 1):
         qs, qe, ks, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
-        nq, nk = qe - qs, ke - ks
-        if nq == 0 or nk == 0:
-            continue
-        kb = k[ks:ke].repeat_interleave(G, dim=1)
-        vb = v[ks:ke].repeat_interleave(G, dim=1)
-        s = torch.einsum("qhd,khd->hqk", q[qs:qe], kb) * scale
-        i = torch.arange(nq)[:, None]
-        j = torch.arange(nk)[None, :]
-        s = s.masked_fill(j > nk - nq + i, float("-inf"))
-        out[qs:qe] = torch.einsum("hqk,khd->qhd", torch.softmax(s, -1), vb)
-    return out.numpy()
+        out[qs:qe] = opa.attend(q[qs:qe], k[ks:ke], v[ks:ke], scale)
+    return out
 
 
 def make(lens_q, lens_k, hq, hkv, dtype=torch.bfloat16, seed=0):
