@@ -12,7 +12,9 @@ Also reported on the same JSON line:
   roofline      the dominant kernel (split-KV attention main kernel): its
                 algorithmic bytes per launch / its average duration, measured
                 with HIP events around each launch on the launching stream
-  cpu_baseline  the numpy oracle (fp32) on host cores over a bounded sample
+  cpu_baseline  the reference's CPU path restated in torch fp32 (oracle/torch_cpu.py)
+                on the host: the whole C2 B=32 step, median of 5 after 2 warm-ups
+                (extra.cpu_baselines: C1, C3, the slot scatter, C4 at M 1 / 56)
   extra         C3 verify, C4 W8A16 (all shapes x M, cold weights), C5 draft
                 chain (us per draft step, attention / GEMV shares) and the
                 attention op split into main + combine
@@ -48,7 +50,6 @@ def parse():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-draft-chain", action="store_true",
                     help="skip the C5 draft-chain extra (its thousands of launches swamp a trace)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-pass", action="store_true")
     return ap.parse_args()
 
@@ -138,113 +139,137 @@ def load_traffic(kernel_key):
 
 
 # ------------------------------------------------------------------------ CPU baseline
-def cpu_baseline(case, seconds, torch):
-    """numpy oracle (float32) over whole sequences of the C2 case until
-    ``seconds`` of CPU time are spent; GB/s on the same algorithmic bytes."""
-    import numpy as np
-    from oracle import paged_attention as opa
+# The reference's CPU path (nanovllm/kernels/paged_decode_attn.py:472-495: page
+# gather + fp32 softmax attention; quant.py:151-159: fp32 dequantize then
+# matmul; the slot scatter of attention.py:21-30) restated in torch fp32 on the
+# host (oracle/torch_cpu.py), timed under inference_mode: 2 warm-ups, then the
+# median of 5, GB/s on the same algorithmic bytes as the GPU rows. The thread
+# count is torch's (OMP_NUM_THREADS: the CPU share the box gives one GPU).
+def _cpu_info(torch):
+    model = ""
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        threads = 1
-    bt = case["tables"][0]
-    lens = case["lens"].tolist()
-    hq, hkv, d = case["num_q_heads"], case["num_kv_heads"], case["head_dim"]
-    q = case["q"].float().cpu().numpy()
-    host = {}  # sequence -> its pages on the host (copied once, outside the timing)
-    done_bytes, spent, seqs = 0, 0.0, 0
-    b = 0
-    while spent < seconds and seqs < 100000:
-        L = lens[b]
-        if b not in host:
-            pages = bt[b, :math.ceil(L / 256)].long().to(case["k_cache"].device)
-            host[b] = (case["k_cache"][pages].float().cpu().numpy(),
-                       case["v_cache"][pages].float().cpu().numpy(),
-                       np.arange(len(pages)).reshape(1, -1))
-        kc, vc, table = host[b]
-        t0 = time.perf_counter()
-        opa.paged_attention(q[b:b + 1], kc, vc, table, [L], case["scale"], dtype=np.float32)
-        spent += time.perf_counter() - t0
-        done_bytes += attn_bytes([L], hq, hkv, d, 2)
-        seqs += 1
-        b = (b + 1) % len(lens)
-    del host
-    return {"value": round(done_bytes / spent / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"numpy fp32 oracle, {seqs} whole sequences of C2 B={len(lens)} "
-                      f"({spent:.1f} s, {threads} BLAS threads, os.cpu_count()={os.cpu_count()})"}
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "torch_threads": torch.get_num_threads(),
+            "os_cpu_count": os.cpu_count()}
 
 
-def _blas_threads():
-    try:
-        from threadpoolctl import threadpool_info
-        return max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        return 1
-
-
-def cpu_baseline_verify(case, seconds):
-    """numpy oracle (float32) over whole sequences of the C3 verify case (7
-    causal rows each) for about ``seconds``; GB/s on the same algorithmic bytes."""
-    import numpy as np
-    from oracle import paged_attention as opa
-    bt, keys, k = case["table"], case["keys"].tolist(), case["k"] + 1
-    q = case["q"].float().cpu().numpy()
-    host, done, spent, seqs, b = {}, 0, 0.0, 0, 0
-    while spent < seconds and seqs < 100000:
-        L = keys[b]
-        if b not in host:
-            pages = bt[b, :math.ceil(L / 256)].long().to(case["k_cache"].device)
-            host[b] = (case["k_cache"][pages].float().cpu().numpy(),
-                       case["v_cache"][pages].float().cpu().numpy(),
-                       np.arange(len(pages)).reshape(1, -1))
-        kc, vc, table = host[b]
-        t0 = time.perf_counter()
-        opa.paged_attention(q[b * k:(b + 1) * k], kc, vc, table, [L], case["scale"],
-                            np.array([0, k]), dtype=np.float32)
-        spent += time.perf_counter() - t0
-        done += attn_bytes([L], 32, 8, 128, 2, q_rows=k)
-        seqs += 1
-        b = (b + 1) % len(keys)
-    threads = _blas_threads()
-    return {"value": round(done / spent / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"numpy fp32 oracle, {seqs} whole sequences of C3 (7 causal rows each, "
-                      f"{spent:.1f} s, {threads} BLAS threads)"}
-
-
-def cpu_baseline_w8a16(seconds):
-    """numpy oracle (float32 dequantize, then matmul) of the C4 lm_head shape
-    (N 151936, K 1024) at M = 1 and M = 16 on row slices of the weight, about
-    ``seconds`` in all; GB/s on the algorithmic bytes of the rows done."""
-    import numpy as np
-    from oracle import w8a16 as ow8
-    rng = np.random.default_rng(0)
-    N, K, rows = 151936, 1024, 8192
-    w = np.clip(np.round(rng.standard_normal((rows, K)) * 40), -127, 127).astype(np.int8)
-    s = (rng.random(rows) * 3e-3 + 1e-3).astype(np.float32)
-    out = {}
-    for M in (1, 16):
-        x = rng.standard_normal((M, K)).astype(np.float32)
-        done, spent, calls = 0, 0.0, 0
-        while spent < seconds / 2 and calls < 100000:
+def _time_cpu(fn, torch, warm=2, reps=5):
+    import statistics
+    with torch.inference_mode():
+        for _ in range(warm):
+            fn()
+        ts = []
+        for _ in range(reps):
             t0 = time.perf_counter()
-            ow8.int8_linear(x, w, s, dtype=np.float32)
-            spent += time.perf_counter() - t0
-            done += ow8.algorithmic_bytes(M, rows, K)
-            calls += 1
-        out[f"M{M}"] = {"GBps": round(done / spent / 1e9, 3),
-                        "us_full_lm_head": round(spent / calls * N / rows * 1e6, 1)}
-    threads = _blas_threads()
-    return {"value": out["M1"]["GBps"], "unit": "GB/s", "cores": threads, "kind": "port",
-            "by_M": out,
-            "sample": f"numpy fp32 oracle (dequantize then matmul), lm_head K=1024 on "
-                      f"{rows}-row slices, M=1 and M=16, {seconds:.0f} s, {threads} BLAS threads"}
+            fn()
+            ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _host_pages(k_cache, v_cache, tables):
+    """The pages the tables use, copied to the host as fp32 (outside any
+    timing), and the tables remapped onto them."""
+    import torch
+    used = sorted({int(x) for t in tables for x in t.flatten().tolist() if x >= 0})
+    remap = torch.full((k_cache.shape[0],), -1, dtype=torch.int64)
+    remap[torch.tensor(used)] = torch.arange(len(used))
+    idx = torch.tensor(used, device=k_cache.device)
+    kc, vc = k_cache[idx].float().cpu(), v_cache[idx].float().cpu()
+    out = [torch.where(t >= 0, remap[t.clamp(min=0).long()], -1) for t in tables]
+    return kc, vc, out
+
+
+def cpu_baseline_decode(case, torch):
+    """The whole C2 decode step on the host: the slot scatter of the new rows,
+    then attention of every sequence over its pages (the headline line's
+    cpu_baseline)."""
+    from oracle import torch_cpu as otc
+    bt = case["tables"][0]
+    kc, vc, (tbl,) = _host_pages(case["k_cache"], case["v_cache"], [bt])
+    lens = case["lens"]
+    q = case["q"].float().cpu()
+    kn, vn = case["k_new"].float().cpu(), case["v_new"].float().cpu()
+    bs = case["block_size"]
+    slots = torch.tensor([int(tbl[b, (int(L) - 1) // bs]) * bs + (int(L) - 1) % bs
+                          for b, L in enumerate(lens)], dtype=torch.int64)
+
+    def step():
+        otc.store_kvcache(kn, vn, kc, vc, slots)
+        otc.paged_attention(q, kc, vc, tbl, lens, case["scale"])
+    sec = _time_cpu(step, torch)
+    info = _cpu_info(torch)
+    nbytes = decode_bytes(lens.tolist(), case["num_q_heads"], case["num_kv_heads"],
+                          case["head_dim"], 2, len(lens))
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": info["torch_threads"],
+            "kind": "port", "us": round(sec * 1e6, 1),
+            "sample": f"the whole C2 B={len(lens)} decode step (store + attention of every "
+                      f"sequence), torch fp32 on the host (oracle/torch_cpu.py), inference_mode, "
+                      f"median of 5 after 2 warm-ups; {info['cpu_model']}, "
+                      f"{info['torch_threads']} threads (os.cpu_count()={info['os_cpu_count']})"}
+
+
+def cpu_baselines_extra(torch, workloads, verify_case):
+    """The other rows of the CPU-baseline plan: C1 (the fp32 CPU configuration
+    itself), C3 verify, the C2 B=32 slot scatter alone, and C4 dequantize then
+    matmul at every shape for M in {1, 56}."""
+    import math as _m
+    from oracle import torch_cpu as otc
+    info = _cpu_info(torch)
+    rows = {"protocol": "torch fp32 on the host (oracle/torch_cpu.py), inference_mode, median "
+                        "of 5 after 2 warm-ups; GB/s on the GPU rows' algorithmic bytes",
+            **info}
+    # C1: Qwen3-0.6B attention geometry, B=1, L=1000, 64-page pool, 4 permuted pages
+    g = torch.Generator().manual_seed(0)
+    kc = torch.randn((64, 256, 8, 128), generator=g)
+    vc = torch.randn((64, 256, 8, 128), generator=g)
+    q = torch.randn((1, 16, 128), generator=g)
+    bt = torch.randperm(64, generator=g)[:4].view(1, 4)
+    sec = _time_cpu(lambda: otc.paged_attention(q, kc, vc, bt, [1000], 128 ** -0.5), torch)
+    nb = 1000 * 8 * 128 * 4 * 2 + 2 * 16 * 128 * 4
+    rows["C1_decode_fp32"] = {"us": round(sec * 1e6, 1), "GBps": round(nb / sec / 1e9, 3)}
+    # C3 verify: 8 sequences x 7 bottom-right causal rows
+    v = verify_case
+    kcv, vcv, (tv,) = _host_pages(v["k_cache"], v["v_cache"], [v["table"]])
+    qv = v["q"].float().cpu()
+    sec = _time_cpu(lambda: otc.paged_attention(qv, kcv, vcv, tv, v["keys"].tolist(),
+                                                v["scale"], v["cu_q"]), torch)
+    nb = attn_bytes(v["keys"].tolist(), 32, 8, 128, 2, q_rows=v["k"] + 1)
+    rows["C3_verify"] = {"us": round(sec * 1e6, 1), "GBps": round(nb / sec / 1e9, 3)}
+    del kcv, vcv
+    # the slot scatter of C2 B=32 alone (32 new rows into a 2048-page pool slice)
+    pool_k = torch.zeros((300, 256, 8, 128))
+    pool_v = torch.zeros_like(pool_k)
+    kn, vn = torch.randn((32, 8, 128), generator=g), torch.randn((32, 8, 128), generator=g)
+    sl = torch.randperm(300 * 256, generator=g)[:32]
+    sec = _time_cpu(lambda: otc.store_kvcache(kn, vn, pool_k, pool_v, sl), torch)
+    nb = 32 * 8 * 128 * 2 * 2 * 2
+    rows["store_kvcache_C2_B32"] = {"us": round(sec * 1e6, 1), "GBps": round(nb / sec / 1e9, 3)}
+    del pool_k, pool_v
+    # C4: every shape, M in {1, 56}
+    c4 = []
+    for name, N, K in workloads.W8A16_SHAPES:
+        w = torch.clamp(torch.round(torch.randn((N, K), generator=g) * 40), -127, 127) \
+            .to(torch.int8)
+        s = torch.rand((N,), generator=g) * 3e-3 + 1e-3
+        for M in (1, 56):
+            x = torch.randn((M, K), generator=g)
+            sec = _time_cpu(lambda: otc.dequant_linear(x, w, s), torch)
+            nb = N * K + 2 * N + 2 * M * K + 2 * M * N
+            c4.append({"shape": name, "M": M, "us": round(sec * 1e6, 1),
+                       "GBps": round(nb / sec / 1e9, 3)})
+        del w
+    rows["C4_w8a16"] = c4
+    return rows
 
 
 # ----------------------------------------------------------------------------- extras
-def bench_verify(ops, workloads, torch, steps, cpu_seconds=0.0):
+def bench_verify(ops, workloads, torch, steps):
     """C3 verify step (fused store + attention) over 8 disjoint page sets (537 MB
     of K/V in all, more than the 256 MB MALL), the 8 calls back to back in one
     graph so the GPU, not the host's graph launches, sets the time; plus the
@@ -284,8 +309,6 @@ def bench_verify(ops, workloads, torch, steps, cpu_seconds=0.0):
     for twin, key in ((None, "attention_us"), ("main", "main_us"), ("floor", "floor_us")):
         t = time_replays([graph_of(chain(False, twin), torch)], reps, 2, torch) / sets
         res[key] = round(t * 1e3, 2)
-    if cpu_seconds > 0:
-        res["cpu_baseline"] = cpu_baseline_verify(case, cpu_seconds)
     return res
 
 
@@ -612,7 +635,7 @@ def main():
                                      "not measured in this run"},
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds, torch)
+        line["cpu_baseline"] = cpu_baseline_decode(case, torch)
     if not args.no_extra:
         del step_graphs, main_graphs, attn_graphs, step_chain, floor_graphs, combine_graphs
         del twin_ws
@@ -624,15 +647,16 @@ def main():
                  "step_us_one_graph_per_step": round(ms_step_graph * 1e3, 2)}
         del case, kc, vc
         torch.cuda.empty_cache()
-        cpu_s = 0.0 if args.no_cpu_baseline else max(args.cpu_seconds / 2, 1.0)
         extra["decode_batches"] = [bench_decode_batch(ops, workloads, torch, b, args.steps)
                                    for b in (1, 8)]
         torch.cuda.empty_cache()
-        extra["verify"] = bench_verify(ops, workloads, torch, args.steps, cpu_s)
+        extra["verify"] = bench_verify(ops, workloads, torch, args.steps)
         torch.cuda.empty_cache()
         extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100))
-        if cpu_s > 0:
-            extra["w8a16_cpu_baseline"] = cpu_baseline_w8a16(cpu_s)
+        if not args.no_cpu_baseline:
+            extra["cpu_baselines"] = cpu_baselines_extra(torch, workloads,
+                                                         workloads.verify_case(seed=0))
+            torch.cuda.empty_cache()
         torch.cuda.empty_cache()
         extra["verify_batch"] = bench_verify_batch(ops, torch, min(args.steps, 100))
         torch.cuda.empty_cache()

@@ -21,6 +21,9 @@ Modules and the reference code each one restates:
                    (nanovllm/layers/layernorm.py:16-47, rotary_embedding.py:6-48,
                    models/qwen3.py:80-88, activation.py:6-11, sampler.py:6-12)
   bf16             bf16 <-> fp32 bit conversion (round to nearest even)
+  torch_cpu        the same paged attention, dequantize-then-matmul and slot
+                   scatter in torch fp32 on the host: the timed CPU baseline
+                   of bench.py (pinned against the numpy modules above)
 
 How each function is pinned (tests/test_oracle_*.py): against library
 routines (torch scaled_dot_product_attention, torch.nn.functional.linear,
