@@ -331,6 +331,31 @@ int sd_w8a16_rmsnorm_linear(const void* x, int64_t x_stride_m, const void* resid
                             void* stream);
 
 /*
+ * The MLP's gate_up projection with SiluAndMul applied to its output: for
+ * weight w (N, K) = [gate rows; up rows] (N = 2 I),
+ *   y[m, i] = bf16(bf16(silu(g)) * u), g = (a @ w[i]^T) * scale[i],
+ *   u = (a @ w[I + i]^T) * scale[I + i], each rounded to dtype first,
+ * with a = x, or a = RMSNorm(x [+ residual]) when norm_weight is not NULL
+ * (the sd_rmsnorm row; residual_out receives bf16(x + residual) as there).
+ * The layer's post_attention_layernorm, gate_up_proj and act_fn
+ * (models/qwen3.py Qwen3MLP.forward, layers/activation.py:6-11) in one launch;
+ * no counterpart entry in the reference. y equals sd_w8a16_rmsnorm_linear (or
+ * sd_w8a16_linear) followed by sd_silu_mul bit for bit. A wave streams gate
+ * row i together with up row I + i and forms the SiLU of the pair once, so
+ * the down projection reads the activated rows with no SiLU of its own.
+ * Row-streaming path only: one or two rows, M * ceil(K / 1024) <= 4,
+ * per-channel scale, at most 32 MiB of weights, N even; other shapes return
+ * SD_ERR_UNSUPPORTED (the caller runs the two calls). y: (M, N / 2) dtype,
+ * sharing no byte with x, residual or residual_out.
+ */
+int sd_w8a16_gate_up_silu(const void* x, int64_t x_stride_m, const void* residual,
+                          int64_t residual_stride_m, void* residual_out,
+                          int64_t residual_out_stride_m, const void* norm_weight, float eps,
+                          const int8_t* w, int64_t w_stride_n, const void* scale,
+                          int32_t scale_dtype, const void* bias, void* y, int64_t y_stride_m,
+                          int64_t M, int64_t N, int64_t K, int32_t dtype, void* stream);
+
+/*
  * Symmetric int8 weight quantization, the producer of the W8A16 format:
  * `quantize_weight` (nanovllm/layers/quant.py:123-148) and the offline
  * converter's `quantize_tensor` (scripts/quantize_int8.py:53-83). Per row and

@@ -60,6 +60,12 @@ SIGNATURES = {
         _p, _i32, _i32, _p,             # scale, scale_dtype, group_size, bias
         _p, _i64,                       # y, y_stride
         _i64, _i64, _i64, _i32, _p]),   # M, N, K, dtype, stream
+    "sd_w8a16_gate_up_silu": (ctypes.c_int, [
+        _p, _i64, _p, _i64, _p, _i64,   # x, stride, residual, stride, residual_out, stride
+        _p, _f32, _p, _i64,             # norm_weight (or NULL), eps, w, w_stride
+        _p, _i32, _p,                   # scale, scale_dtype, bias
+        _p, _i64,                       # y, y_stride
+        _i64, _i64, _i64, _i32, _p]),   # M, N, K, dtype, stream
     "sd_w8a16_linear": (ctypes.c_int, [
         _p, _i64, _p, _i64,             # x, x_stride, w, w_stride
         _p, _i32, _i32, _p,             # scale, scale_dtype, group_size, bias

@@ -179,21 +179,25 @@ __device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_
 // activation type), the eager module's roundings; g and u are 8 packed 16-bit
 // values each. Shared by the SiLU kernel and the W8A16 activation path that
 // fuses it, so both give the same bits.
+// One element: the fp32 product before its final rounding to T.
+template <typename T>
+__device__ __forceinline__ float silu_mul1(float gv, float uv) {
+#pragma clang fp contract(off)
+  const float sv = static_cast<float>(static_cast<T>(gv / (1.f + expf(-gv))));
+  return sv * uv;
+}
+
 template <typename T>
 __device__ __forceinline__ u32x4 silu_mul8(u32x4 g, u32x4 u) {
-#pragma clang fp contract(off)
   const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float r[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float gv = from_bits<T>(static_cast<uint16_t>(gw[i] >> (16 * h)));
-      const float uv = from_bits<T>(static_cast<uint16_t>(uw[i] >> (16 * h)));
-      const float sv = static_cast<float>(static_cast<T>(gv / (1.f + expf(-gv))));
-      r[h] = sv * uv;
-    }
+    for (int h = 0; h < 2; ++h)
+      r[h] = silu_mul1<T>(from_bits<T>(static_cast<uint16_t>(gw[i] >> (16 * h))),
+                          from_bits<T>(static_cast<uint16_t>(uw[i] >> (16 * h))));
     o[i] = pack2<T>(r[0], r[1]);
   }
   return u32x4{o[0], o[1], o[2], o[3]};

@@ -65,6 +65,9 @@ struct W8Params {
   uint16_t* nres_out;   // (M, K) bf16(x + residual), written by workgroup x = 0, or NULL
   int64_t nres_out_s;
   float neps;
+  // paired rows (gate_up with the SiluAndMul epilogue): output column i pairs
+  // weight rows i and i + pair; N is the number of pairs (output columns)
+  int32_t pair;
 };
 
 __device__ __forceinline__ float load_scale(const void* s, int dtype, int64_t i) {
@@ -519,15 +522,24 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 // Per-channel scales only (applied to the reduced sum).
 template <int MR, int C, int R>
 struct RowsShape {
-  static constexpr int V = R * MR;  // sums per lane per batch
+  static constexpr int V = R * MR;  // sums per lane per batch (R: rows of a batch)
   static constexpr int LV = V == 16 ? 4 : (V == 8 ? 3 : (V == 4 ? 2 : (V == 2 ? 1 : 0)));
   static_assert((1 << LV) == V, "R * MR must be a power of two <= 16");
 };
 
-template <typename T, int MR, int C, int R, int MODE>
+// PAIR (the gate_up projection with SiluAndMul, sd_w8a16_gate_up_silu): a
+// wave owns output columns i (weight rows i and i + p.pair); a batch holds
+// R / 2 gate rows then the R / 2 matching up rows. After the reduce-scatter
+// the gate sum of a pair sits 32 lanes below its up sum, so one xor-32
+// shuffle brings them together and the lower lane writes
+// bf16(bf16(silu(g)) * u) of the two bf16-rounded sums — the bits that the
+// linear followed by the SiLU kernel give.
+template <typename T, int MR, int C, int R, int MODE, bool PAIR = false>
 __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int rows_per_wave) {
 #pragma clang fp contract(off)
   constexpr int V = RowsShape<MR, C, R>::V, LV = RowsShape<MR, C, R>::LV;
+  constexpr int RP = PAIR ? R / 2 : R;  // output rows (pairs) per batch
+  static_assert(!PAIR || (R % 2 == 0 && V / 2 * (64 >> LV) == 32), "pairs 32 lanes apart");
   const int lane = threadIdx.x & 63;
   const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
   const int r0 = gw * rows_per_wave;
@@ -629,11 +641,16 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
     }
   }
 
+  // weight row of batch row r for the output rows starting at rb
+  auto wrow = [&](int rb, int r) -> int64_t {
+    const int64_t o = min(rb + (PAIR ? r % RP : r), r1 - 1);
+    return PAIR && r >= RP ? o + p.pair : o;
+  };
   // ---- weight rows, R per batch, two batches in flight
   auto load = [&](u32x4 (&B)[R][C], int rb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t row = min(rb + r, r1 - 1);
+      const int64_t row = wrow(rb, r);
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const int k0 = min(c * 1024 + 16 * lane, p.K - 16);  // lanes past K: a valid address, unused
@@ -645,7 +662,6 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
     float acc[V];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t row = min(rb + r, r1 - 1);
 #pragma unroll
       for (int m = 0; m < MR; ++m) acc[r * MR + m] = 0.f;
 #pragma unroll
@@ -678,7 +694,19 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
     float v = acc[0];
 #pragma unroll
     for (int off = 32 >> LV; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    if ((lane & ((64 >> LV) - 1)) == 0) {
+    if constexpr (PAIR) {
+      // every lane scales its sum, the gate half pairs with the up half
+      const int idx = lane >> (6 - LV);
+      const int r = idx / MR, m = idx - r * MR;
+      const int64_t row = wrow(rb, r);
+      v = v * load_scale(p.scale, p.scale_dtype, row);
+      if (p.bias) v = v + sd::from_bits<T>(p.bias[row]);
+      const float vb = sd::from_bits<T>(sd::to_bits<T>(v));  // the linear's rounding
+      const float ub = __shfl_xor(vb, 32);
+      const int orow = rb + r;
+      if ((lane & ((64 >> LV) - 1)) == 0 && r < RP && orow < r1 && m < p.M)
+        p.y[static_cast<int64_t>(m) * p.ys + orow] = sd::to_bits<T>(sd::silu_mul1<T>(vb, ub));
+    } else if ((lane & ((64 >> LV) - 1)) == 0) {
       const int idx = lane >> (6 - LV);
       const int r = idx / MR, m = idx - r * MR;
       const int row = rb + r;
@@ -691,12 +719,12 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
   };
   u32x4 ba[R][C], bb[R][C];
   load(ba, r0);
-  for (int rb = r0; rb < r1; rb += 2 * R) {
-    load(bb, rb + R < r1 ? rb + R : rb);
+  for (int rb = r0; rb < r1; rb += 2 * RP) {
+    load(bb, rb + RP < r1 ? rb + RP : rb);
     consume(ba, rb);
-    if (rb + R >= r1) break;
-    load(ba, rb + 2 * R < r1 ? rb + 2 * R : rb);
-    consume(bb, rb + R);
+    if (rb + RP >= r1) break;
+    load(ba, rb + 2 * RP < r1 ? rb + 2 * RP : rb);
+    consume(bb, rb + RP);
   }
 }
 
@@ -900,15 +928,22 @@ bool rows_eligible(const W8Params& p) {
   return p.group == 0;
 }
 
-template <typename T, int MR, int C, int MODE>
+template <typename T, int MR, int C, int MODE, bool PAIR = false>
 int launch_rows_c(const W8Params& p, hipStream_t st) {
-  // about 4 rows per wave, at most two waves per SIMD (8 per CU)
+  // about 4 weight rows per wave (2 output pairs with PAIR), at most two waves
+  // per SIMD (8 per CU)
   int64_t waves = static_cast<int64_t>(sd::device_cus()) * 8;
-  const int64_t want = (static_cast<int64_t>(p.N) + 3) / 4;
+  const int64_t want = PAIR ? (static_cast<int64_t>(p.N) + 1) / 2
+                            : (static_cast<int64_t>(p.N) + 3) / 4;
   if (want < waves) waves = want;
   const int blocks = static_cast<int>((waves + kWaves - 1) / kWaves);
   const int rpw = static_cast<int>((p.N + static_cast<int64_t>(blocks) * kWaves - 1) /
                                    (static_cast<int64_t>(blocks) * kWaves));
+  if constexpr (PAIR) {
+    hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 8, MODE, true>), dim3(blocks),
+                       dim3(kThreads), 0, st, p, rpw);
+    return SD_OK;
+  }
   if constexpr (MR == 1 && C == 1) {
     if (rpw >= 32) {
       hipLaunchKernelGGL((w8a16_rows_kernel<T, 1, 1, 8, MODE>), dim3(blocks), dim3(kThreads),
@@ -921,19 +956,20 @@ int launch_rows_c(const W8Params& p, hipStream_t st) {
   return SD_OK;
 }
 
-template <typename T, int MODE>
+template <typename T, int MODE, bool PAIR = false>
 int launch_rows(const W8Params& p, hipStream_t st) {
   const int C = (p.K + 1023) / 1024;
   int rc;
   if (p.M == 1) {
     switch (C) {
-      case 1: rc = launch_rows_c<T, 1, 1, MODE>(p, st); break;
-      case 2: rc = launch_rows_c<T, 1, 2, MODE>(p, st); break;
-      case 3: rc = launch_rows_c<T, 1, 3, MODE>(p, st); break;
-      default: rc = launch_rows_c<T, 1, 4, MODE>(p, st); break;
+      case 1: rc = launch_rows_c<T, 1, 1, MODE, PAIR>(p, st); break;
+      case 2: rc = launch_rows_c<T, 1, 2, MODE, PAIR>(p, st); break;
+      case 3: rc = launch_rows_c<T, 1, 3, MODE, PAIR>(p, st); break;
+      default: rc = launch_rows_c<T, 1, 4, MODE, PAIR>(p, st); break;
     }
   } else {
-    rc = C == 1 ? launch_rows_c<T, 2, 1, MODE>(p, st) : launch_rows_c<T, 2, 2, MODE>(p, st);
+    rc = C == 1 ? launch_rows_c<T, 2, 1, MODE, PAIR>(p, st)
+                : launch_rows_c<T, 2, 2, MODE, PAIR>(p, st);
   }
   if (rc != SD_OK) return rc;
   return sd::check_launch("w8a16 rows");
@@ -941,6 +977,10 @@ int launch_rows(const W8Params& p, hipStream_t st) {
 
 template <typename T>
 int launch_rows_any(const W8Params& p, int mode, hipStream_t st) {
+  if (p.pair > 0) {  // gate_up with the SiLU epilogue: plain or norm activations
+    if (mode == 2) return launch_rows<T, 2, true>(p, st);
+    return launch_rows<T, 0, true>(p, st);
+  }
   if (mode == 1) return launch_rows<T, 1>(p, st);
   if (mode == 2) return launch_rows<T, 2>(p, st);
   return launch_rows<T, 0>(p, st);
@@ -970,10 +1010,12 @@ struct NormArgs {
   float eps;
 };
 
+// pair: the gate_up projection with the SiLU epilogue (N weight rows, N / 2
+// output columns; row-streaming path only)
 int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& norm,
               const int8_t* w, int64_t w_stride_n, const void* scale, int32_t scale_dtype,
               int32_t group_size, const void* bias, void* y, int64_t y_stride_m, int64_t M,
-              int64_t N, int64_t K, int32_t dtype, void* stream) {
+              int64_t N, int64_t K, int32_t dtype, void* stream, bool pair = false) {
   if (M < 0 || N <= 0 || K <= 0 || group_size < 0) {
     sd::set_error("w8a16: invalid sizes M=%lld N=%lld K=%lld group=%d", (long long)M,
                   (long long)N, (long long)K, group_size);
@@ -1014,7 +1056,8 @@ int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& nor
   // residual_out, so no output may share a byte with an input or with the
   // other output.
   const int64_t xw = up >= 0 ? up + K : K;
-  const sd::Span sx = sd::span16(x, M, x_stride_m, xw), sy = sd::span16(y, M, y_stride_m, N);
+  const sd::Span sx = sd::span16(x, M, x_stride_m, xw),
+                 sy = sd::span16(y, M, y_stride_m, pair ? N / 2 : N);
   const sd::Span sr = sd::span16(norm.residual, M, norm.residual_stride, K);
   const sd::Span sro = sd::span16(norm.residual_out, M, norm.residual_out_stride, K);
   if (sy.overlaps(sx) || sy.overlaps(sr) || sy.overlaps(sro) || sro.overlaps(sx) ||
@@ -1052,8 +1095,22 @@ int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& nor
   p.nres_out = static_cast<uint16_t*>(norm.residual_out);
   p.nres_out_s = norm.residual_out_stride;
   p.neps = norm.eps;
+  p.pair = 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int mode = up >= 0 ? 1 : (p.nw ? 2 : 0);
+  if (pair) {
+    if (N % 2 != 0 || !rows_eligible(p)) {
+      sd::set_error("w8a16_gate_up_silu: the SiLU epilogue runs on the row-streaming path "
+                    "(one or two rows, M * ceil(K / 1024) <= 4, per-channel scales, at most "
+                    "32 MiB of weights, N even); got M=%lld N=%lld K=%lld group=%d",
+                    (long long)M, (long long)N, (long long)K, group_size);
+      return SD_ERR_UNSUPPORTED;
+    }
+    p.pair = static_cast<int32_t>(N / 2);
+    p.N = static_cast<int32_t>(N / 2);
+    if (dtype == SD_BF16) return launch_rows_any<__bf16>(p, mode, st);
+    return launch_rows_any<_Float16>(p, mode, st);
+  }
   if (rows_eligible(p)) {
     if (dtype == SD_BF16) return launch_rows_any<__bf16>(p, mode, st);
     return launch_rows_any<_Float16>(p, mode, st);
@@ -1122,4 +1179,34 @@ extern "C" int sd_w8a16_rmsnorm_linear(const void* x, int64_t x_stride_m, const 
                       residual_out_stride_m, eps};
   return run_w8a16(x, x_stride_m, -1, norm, w, w_stride_n, scale, scale_dtype, group_size, bias, y,
                    y_stride_m, M, N, K, dtype, stream);
+}
+
+extern "C" int sd_w8a16_gate_up_silu(const void* x, int64_t x_stride_m, const void* residual,
+                                     int64_t residual_stride_m, void* residual_out,
+                                     int64_t residual_out_stride_m, const void* norm_weight,
+                                     float eps, const int8_t* w, int64_t w_stride_n,
+                                     const void* scale, int32_t scale_dtype, const void* bias,
+                                     void* y, int64_t y_stride_m, int64_t M, int64_t N,
+                                     int64_t K, int32_t dtype, void* stream) {
+  sd::clear_error();
+  if (norm_weight && (K % 8 != 0 || K > 8192)) {
+    sd::set_error("w8a16_gate_up_silu: the norm needs K a multiple of 8 up to 8192 (K=%lld)",
+                  (long long)K);
+    return SD_ERR_UNSUPPORTED;
+  }
+  if ((residual || residual_out) && !norm_weight) {
+    sd::set_error("w8a16_gate_up_silu: a residual needs the norm weight");
+    return SD_ERR_VALUE;
+  }
+  if ((residual && (!sd::aligned16(residual) || residual_stride_m % 8)) ||
+      (residual_out && (!sd::aligned16(residual_out) || residual_out_stride_m % 8)) ||
+      (norm_weight && !sd::aligned16(norm_weight))) {
+    sd::set_error("w8a16_gate_up_silu: residual, residual_out and norm weight rows 16-byte "
+                  "aligned");
+    return SD_ERR_UNSUPPORTED;
+  }
+  const NormArgs norm{norm_weight, residual, residual_stride_m, residual_out,
+                      residual_out_stride_m, eps};
+  return run_w8a16(x, x_stride_m, -1, norm, w, w_stride_n, scale, scale_dtype, 0, bias, y,
+                   y_stride_m, M, N, K, dtype, stream, true);
 }

@@ -27,9 +27,9 @@ memset, which a captured graph does not replay reliably), or this library's
 fused neighbour kernels with ``fused=True``:
 add + RMSNorm inside the projection that consumes it (qkv, gate_up, lm_head;
 at up to 4 rows, two launches beyond), q/k norm + RoPE + store_kvcache in one
-launch on the qkv output (the attention reads q through strides), SiLU*mul
-inside the down projection, the sampler's argmax; the embedding lookup stays a
-torch index.
+launch on the qkv output (the attention reads q through strides), SiLU*mul in
+the gate_up projection's epilogue (one or two rows; the SiLU launch beyond),
+the sampler's argmax; the embedding lookup stays a torch index.
 
 ``chain()`` runs ``k`` steps back to back, each feeding its tokens to the next,
 on static buffers, so the whole chain can be captured in one HIP graph.
@@ -253,10 +253,12 @@ class DraftChain:
                                     self.scale, context_lens=ctx)
             h = ops.w8a16_linear(o.reshape(B, Hq * D), *lw["o"])
             ro, ping = self._res[ping], ping ^ 1
-            gu = ops.w8a16_rmsnorm_linear(h, lw["post_norm"], eps, *lw["gate_up"],
-                                          residual=residual, residual_out=ro)
+            # add + RMSNorm, gate_up and SiLU*mul in one launch (paired gate / up
+            # rows) at one or two rows, then the plain down projection
+            act = ops.w8a16_gate_up_silu(h, *lw["gate_up"], lw["post_norm"], eps,
+                                         residual=residual, residual_out=ro)
             residual = ro
-            h = ops.w8a16_silu_linear(gu, *lw["down"])
+            h = ops.w8a16_linear(act, *lw["down"])
         logits = ops.w8a16_rmsnorm_linear(h, self.final_norm, eps, *self.lm_head,
                                           residual=residual)
         ops.sample(logits, out=self.tokens[s + 1])

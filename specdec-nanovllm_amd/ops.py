@@ -436,6 +436,68 @@ def w8a16_rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     return y.view(shape)
 
 
+def w8a16_gate_up_silu(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
+                       norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                       residual: torch.Tensor | None = None,
+                       residual_out: torch.Tensor | None = None,
+                       bias: torch.Tensor | None = None,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu_mul(w8a16_linear(a, qweight, scale)) of the MLP (models/qwen3.py
+    Qwen3MLP.forward: gate_up_proj then act_fn), with a = x, or a =
+    rmsnorm(x, norm_weight, eps, residual) when ``norm_weight`` is given
+    (``residual_out`` as in ``w8a16_rmsnorm_linear``). qweight (2I, K) =
+    [gate; up], per-channel scale (2I,); returns (..., I), bit for bit the
+    separate calls. One launch on the row-streaming path (one or two rows,
+    weights up to 32 MiB): a wave streams gate row i with up row I + i and
+    forms the pair's SiLU once; other shapes take the separate launches."""
+    assert qweight.dtype == torch.int8 and qweight.dim() == 2
+    N, K = qweight.shape
+    assert N % 2 == 0 and x.shape[-1] == K
+    assert residual_out is None or residual is not None, "residual_out needs a residual"
+    assert residual is None or norm_weight is not None, "a residual needs the norm weight"
+    x2 = _rows16(x, "x")
+    M = x2.shape[0]
+    nw = None if norm_weight is None else norm_weight.to(x.dtype).contiguous()
+    qw = qweight if qweight.is_contiguous() else qweight.contiguous()
+    sc = scale.contiguous()
+    assert sc.numel() == N, "per-channel scale must have N entries"
+    r2 = ro = None
+    if residual is not None:
+        assert residual.shape == x.shape and residual.dtype == x.dtype
+        r2 = _rows16(residual, "residual")
+    if residual_out is not None:
+        assert residual_out.shape == x.shape and residual_out.dtype == x.dtype
+        ro = residual_out.reshape(M, K)
+        assert ro.stride(-1) == 1 and ro.data_ptr() % 16 == 0 and (M <= 1 or ro.stride(0) % 8 == 0)
+    b = None if bias is None else bias.to(x.dtype).contiguous()
+    dev = _lib.require_device(x2, nw, qw, sc, b, r2, ro, out)
+    shape = (*x.shape[:-1], N // 2)
+    if out is None:
+        y = torch.empty((M, N // 2), device=dev, dtype=x.dtype)
+    else:
+        y = out.reshape(M, N // 2)
+        assert y.dtype == x.dtype and y.stride(-1) == 1
+    if M == 0:
+        return y.view(shape)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.sd_w8a16_gate_up_silu(
+            x2.data_ptr(), x2.stride(0), _ptr(r2), 0 if r2 is None else r2.stride(0),
+            _ptr(ro), 0 if ro is None else ro.stride(0), _ptr(nw), float(eps),
+            qw.data_ptr(), qw.stride(0), sc.data_ptr(), _lib.dtype_code(sc.dtype), _ptr(b),
+            y.data_ptr(), y.stride(0), M, N, K, _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
+    if rc == _lib.SD_ERR_UNSUPPORTED and (nw is None or (K % 8 == 0 and K <= 8192)):
+        # not on the row-streaming path: the projection, then the SiLU launch
+        if nw is None:
+            gu = w8a16_linear(x2, qw, sc, b)
+        else:
+            gu = w8a16_rmsnorm_linear(x2, nw, eps, qw, sc, b, residual=r2, residual_out=ro)
+        silu_mul(gu, out=y)
+        return y.view(shape)
+    _lib.check(rc)
+    return y.view(shape)
+
+
 def quantize_int8(w: torch.Tensor, group_size: int = 0):
     """Symmetric int8 quantization of a 2-D weight on the GPU (the W8A16
     format's producer, nanovllm/layers/quant.py:123-148): per row (group_size

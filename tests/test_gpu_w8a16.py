@@ -290,3 +290,49 @@ def test_row_streaming_path(M, K, gs, act):
     y = ops.w8a16_linear(c["x"], c["w"], s, bias, group_size=gs)
     check(y, c["x"], c["w"], s, bias, "per_group" if gs else "per_channel", gs,
           out_rel=2.0 ** -9 if act == torch.float16 else 2.0 ** -8, what=f"rows M={M} K={K} gs={gs}")
+
+
+@pytest.mark.parametrize("M,N,K,act,norm,res", [(1, 6144, 1024, torch.bfloat16, True, True),
+                                                (1, 6144, 1024, torch.bfloat16, False, False),
+                                                (2, 6144, 1024, torch.float16, True, True),
+                                                (1, 2048, 2048, torch.float16, True, False),
+                                                (2, 512, 2048, torch.bfloat16, False, False),
+                                                (1, 8192, 4096, torch.bfloat16, True, True),
+                                                (1, 272, 1024, torch.bfloat16, True, True),
+                                                (3, 6144, 1024, torch.bfloat16, True, True),
+                                                (16, 6144, 1024, torch.float16, True, True)])
+def test_gate_up_silu_is_linear_then_silu_mul(M, N, K, act, norm, res):
+    """The gate_up projection with the SiLU epilogue (paired gate / up rows on
+    the row-streaming path; the separate launches past it) equals the
+    projection (with its RMSNorm) followed by the SiLU kernel, bit for bit."""
+    c = workloads.w8a16_case(M, N, K, seed=M * 7 + N, act_dtype=act)
+    g = workloads.device_generator(DEV, 31)
+    x = (torch.randn((M, K), generator=g, device=DEV) * 2).to(act)
+    r = torch.randn((M, K), generator=g, device=DEV).to(act) if res else None
+    nw = (1 + 0.1 * torch.randn((K,), generator=g, device=DEV)).to(act) if norm else None
+    bias = torch.randn((N,), generator=g, device=DEV).to(act) if M == 2 else None
+    if norm:
+        ro_two = torch.empty_like(x) if res else None
+        gu = ops.w8a16_rmsnorm_linear(x, nw, 1e-6, c["w"], c["s"], bias, residual=r,
+                                      residual_out=ro_two)
+    else:
+        gu = ops.w8a16_linear(x, c["w"], c["s"], bias)
+    two = ops.silu_mul(gu)
+    ro = torch.empty_like(x) if res else None
+    got = ops.w8a16_gate_up_silu(x, c["w"], c["s"], nw, 1e-6, residual=r, residual_out=ro,
+                                 bias=bias)
+    assert got.shape == (M, N // 2)
+    assert torch.equal(got.view(torch.int16), two.view(torch.int16))
+    if res:
+        assert torch.equal(ro, ro_two)
+
+
+def test_gate_up_silu_entry_refuses_shapes_off_the_row_path():
+    c = workloads.w8a16_case(3, 2048, 1024, seed=5)
+    y = torch.empty((3, 1024), dtype=torch.float16, device=DEV)
+    lib = _lib.load()
+    rc = lib.sd_w8a16_gate_up_silu(c["x"].data_ptr(), c["x"].stride(0), None, 0, None, 0, None,
+                                   1e-6, c["w"].data_ptr(), c["w"].stride(0), c["s"].data_ptr(),
+                                   _lib.dtype_code(c["s"].dtype), None, y.data_ptr(), y.stride(0),
+                                   3, 2048, 1024, _lib.SD_F16, _lib.stream_ptr(torch.device(DEV)))
+    assert rc == _lib.SD_ERR_UNSUPPORTED and b"row-streaming" in lib.sd_last_error()
