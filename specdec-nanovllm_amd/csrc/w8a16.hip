@@ -559,6 +559,15 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
       // waves 0 / 1 (even c) and 2 / 3 (odd c), and its xor steps 32 .. 2
       // are lane xor 16 .. 1 here, step 1 the e pair
       float ss[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [c % 2][e]
+      // the norm weight's columns load with the activations (one round trip)
+      u32x4 nwq[C][2];
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int k0 = c * 1024 + 16 * lane + 8 * e;
+          nwq[c][e] = k0 < p.K ? sd::load16(p.nw + k0) : u32x4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const int k0 = c * 1024 + 16 * lane;
@@ -610,7 +619,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           if (k0 + 8 * e < p.K) {
-            const u32x4 wq = sd::load16(p.nw + k0 + 8 * e);
+            const u32x4 wq = nwq[c][e];
             const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
