@@ -84,6 +84,20 @@ __device__ __forceinline__ void store16(void* p, u32x4 v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
 
+// `keep ? off : 0` for a load offset, formed without a branch. The compiler
+// turns a select whose operand is an address computation into a branch around
+// it, and the join after such a branch copies the loaded registers, which waits
+// for every vector load in flight (s_waitcnt vmcnt(0)): the prefetch issued one
+// step earlier then lands before the next one is issued. An opaque mask keeps
+// the select an AND; the offset (not the pointer) is masked so that the load
+// stays a global one (a pointer rebuilt from an integer loads through the flat
+// path, which the compiler also waits for in full).
+__device__ __forceinline__ int64_t keep_or_zero(bool keep, int64_t off) {
+  uint32_t m = keep ? ~0u : 0u;
+  asm("" : "+v"(m));
+  return static_cast<int64_t>(static_cast<uint64_t>(off) & ((static_cast<uint64_t>(m) << 32) | m));
+}
+
 // Orders LDS traffic between the lanes of one wave (a wave-private LDS tile
 // written by some lanes and read by others): a compiler barrier plus the
 // wavefront-scope fences of the AMDGPU memory model.

@@ -126,8 +126,8 @@ template <> __device__ __forceinline__ u32x4 dequant8<__bf16>(uint32_t w0, uint3
 // (SWZ = min(4 U, 16) - 1), from which each lane reads its MFMA A operand
 // (16 int8 of row l % 16 at k = 64 step + 16 (l / 16)) with ds_read_b128; with
 // 16 positions per row the 16 lanes of a read hit distinct banks.
-// The exception is the staged form with 32 activation rows (XL, MT = 2): there
-// each lane loads its A operand directly (a load instruction then covers 16
+// The exception is the staged form with 32 or 64 activation rows (XL, MT >= 2):
+// there each lane loads its A operand directly (a load instruction then covers 16
 // rows x 64 bytes, half cache lines, which costs the narrower shapes 2-20%),
 // because without the weight tile two workgroups fit per CU beside the
 // 64 KB of activation rows, and the MFMA work per weight byte is twice that of
@@ -257,14 +257,14 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t ko = static_cast<int64_t>(min(s0 + u, p.nks - 1)) * 64 + lg * 16;
-        R.w[nt * U + u] = sd::load16_stream(real ? p.w + static_cast<int64_t>(n) * p.ws + ko : p.w);
+        R.w[nt * U + u] = sd::load16_stream(p.w + sd::keep_or_zero(real, static_cast<int64_t>(n) * p.ws + ko));
       }
     }
     } else {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int n = min(n0 + i * RPI + ld_row, p.N - 1);
-      R.w[i] = sd::load16_stream(real ? p.w + static_cast<int64_t>(n) * p.ws + kw_off : p.w);
+      R.w[i] = sd::load16_stream(p.w + sd::keep_or_zero(real, static_cast<int64_t>(n) * p.ws + kw_off));
     }
     }
 #pragma unroll
@@ -492,17 +492,29 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
     __syncthreads();
     if (nit == 0) return;
   }
-  for (int it = 0; it < nit; it += D) {
+  // Whole rounds of D items, then the last nit % D items (already loaded) after
+  // the loop: an exit from inside a round would reach the loop head with this
+  // round's loads still in flight, and the compiler then waits for every load
+  // at the head, the prefetch of the next item included.
+  int it = 0;
+  for (; it + D <= nit; it += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int cur = it + d;
-      if (cur >= nit) break;  // wave-uniform (workgroup-uniform when KW > 1)
       const int ahead = min(cur + D - 1, nit - 1);  // past the end: dummy loads
       load(ring[(d + D - 1) % D], group_of(ahead), ahead % nchunks, cur + D - 1 < nit);
       const int gi = group_of(cur), ci = cur % nchunks;
       compute(ring[d], gi, ci);
       if (ci + 1 == nchunks) epilogue(gi);
     }
+  }
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) {
+    const int cur = it + d;
+    if (cur >= nit) break;  // wave-uniform (workgroup-uniform when KW > 1)
+    const int gi = group_of(cur), ci = cur % nchunks;
+    compute(ring[d], gi, ci);
+    if (ci + 1 == nchunks) epilogue(gi);
   }
 }
 
@@ -749,12 +761,13 @@ struct W8Plan {
 
 W8Plan make_plan(int64_t M, int64_t N, int64_t K) {
   W8Plan pl;
-  // Activation rows in blocks of 16 (MT = 1) or 32 (MT = 2) along grid.y: a
-  // 64-row tile needs more registers than 2 waves per SIMD allow. The blocks
-  // of one row group run at the same time on the same XCD (launch_k sizes the
-  // grid to one resident set with grid.x a multiple of 8), so mostly only the
-  // first reads the weights from HBM; the others hit L2.
-  pl.MT = M <= 16 ? 1 : 2;
+  // Activation rows in blocks of 16 (MT = 1), 32 (MT = 2) or 64 (MT = 4) along
+  // grid.y. Every block streams the whole weight matrix, and a second block
+  // only hits L2 while it runs in step with the first: with the weight loads
+  // pipelined the blocks drift apart (lm_head M = 56 as two 32-row blocks
+  // fetched 1.75x the weight bytes from HBM), so up to 64 rows (K <= 1024,
+  // staged in one workgroup's LDS) are one block.
+  pl.MT = M <= 16 ? 1 : (M <= 32 || K > 1024 || N <= 16 ? 2 : 4);
   pl.mblocks = static_cast<int>((M + pl.MT * 16 - 1) / (pl.MT * 16));
   const int64_t nr = (N + 15) / 16;
   const int cus = sd::device_cus();
@@ -819,6 +832,8 @@ int resident_wgs(Kern kern) {
 // workgroup stages (32 rows of K <= 1024).
 constexpr int kXPad = 16;
 constexpr int kXlMaxBytes = 32 * (1024 * 2 + kXPad);
+// 64-row blocks (MT = 4): one workgroup per CU holds the rows.
+constexpr int kXlMaxBytes64 = 64 * (1024 * 2 + kXPad);
 // K-split kernels (narrow layers, about one row group per workgroup) stage only
 // when the activation block is large enough to pay for the staging (M > 16
 // rows) and small enough to stage fast (16 rows of K <= 1024), or when the
@@ -848,12 +863,14 @@ int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
     // occupancy matters); K-split kernels as kXlMaxBytesSplit says
     const int rows = static_cast<int>(p.M < MT * 16 ? p.M : MT * 16);
     const size_t xbytes = static_cast<size_t>(rows) * p.xpitch;
-    const size_t xmax = static_cast<size_t>(KW == 1 ? kXlMaxBytes : kXlMaxBytesSplit);
+    const size_t xmax = static_cast<size_t>(KW == 1 ? (MT == 4 ? kXlMaxBytes64 : kXlMaxBytes)
+                                                    : kXlMaxBytesSplit);
     if (p.xpitch > 0 && xbytes <= xmax && (KW == 1 || MODE != 0 || p.M > 16)) {
-      // 32 staged rows (MT = 2) load the weights straight into MFMA operand
-      // order, no weight tile: two workgroups per CU fit beside the rows, and
-      // 2-step chunks measured best there (lm_head M = 56: 63.8 us; 8-step
-      // chunks through the tile at one workgroup per CU: 77.8 us)
+      // 32 or 64 staged rows (MT >= 2) load the weights straight into MFMA
+      // operand order, no weight tile: two workgroups per CU fit beside 32
+      // rows, one beside 64, and 2-step chunks measured best there (lm_head
+      // M = 56, two 32-row blocks before the loads were pipelined: 63.8 us;
+      // 8-step chunks through the tile at one workgroup per CU: 77.8 us)
       constexpr int UX = MT >= 2 ? 2 : U;
       constexpr int NSUB = kWaves / KW;
       auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true, MODE>;
@@ -901,6 +918,7 @@ int launch_kw(const W8Params& p, const W8Plan& pl, dim3 grid, hipStream_t st) {
       case 1 * 8 + 1: return launch_k<T, 1, 1, 1, PG, MODE>(p, grid, st);
       case 1 * 8 + 2: return launch_k<T, 1, 2, 1, PG, MODE>(p, grid, st);
       case 2 * 8 + 1: return launch_k<T, 2, 1, 1, PG, MODE>(p, grid, st);
+      case 4 * 8 + 2: return launch_k<T, 4, 2, 1, PG, MODE>(p, grid, st);
       default: return launch_k<T, 2, 2, 1, PG, MODE>(p, grid, st);
     }
   } else {

@@ -75,11 +75,12 @@ def test_ragged_shapes_and_bias(M, N, K):
     check(y, c["x"], c["w"], c["s"], bias, what=f"{M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("M", [1, 3, 12, 40])
+@pytest.mark.parametrize("M", [1, 3, 12, 33, 40, 64, 65])
 @pytest.mark.parametrize("gs", [0, 64, 128])
 def test_wide_path_scales_and_bias(M, gs):
     # N = 33000 rows of K = 1024: the wide path (whole rows per wave, activation rows and
-    # the row groups' scales and bias staged in LDS), ragged last row group, fp32 scales
+    # the row groups' scales and bias staged in LDS), ragged last row group, fp32 scales;
+    # 33..64 rows are one 64-row block, 65 two
     N, K = 33000, 1024
     c = workloads.w8a16_case(M, N, K, seed=M + gs)
     g = workloads.device_generator(DEV, 11)
@@ -162,7 +163,8 @@ def test_errors():
                                           (7, 1024, 3072, 0, torch.float16),
                                           (56, 1024, 3072, 0, torch.bfloat16),
                                           (3, 33000, 1024, 0, torch.bfloat16),
-                                          (20, 33000, 1024, 128, torch.float16)])
+                                          (20, 33000, 1024, 128, torch.float16),
+                                          (40, 33000, 1024, 0, torch.bfloat16)])
 def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
     # the down projection fed straight from gate_up (narrow K-split path and the
     # wide path with staged activations): bit-identical to the two-launch form
@@ -194,7 +196,8 @@ def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
                                               (3, 512, 1152, 0, torch.float16, True),
                                               (2, 1024, 8192, 0, torch.bfloat16, False),
                                               (9, 33000, 1024, 128, torch.float16, True),
-                                              (24, 33000, 1024, 0, torch.bfloat16, True)])
+                                              (24, 33000, 1024, 0, torch.bfloat16, True),
+                                              (48, 33000, 1024, 0, torch.bfloat16, True)])
 def test_rmsnorm_linear_is_rmsnorm_then_linear(M, N, K, gs, act, res):
     # add + RMSNorm formed while staging: bit-identical to rmsnorm then the
     # linear, residual_out identical to rmsnorm's (one row block per 16 or 32
