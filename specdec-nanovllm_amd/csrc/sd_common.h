@@ -123,8 +123,9 @@ __device__ __forceinline__ float sum_over_groups(float v) {
 // results below 2^-126 flush to 0, 2^-inf = 0. Softmax weights only.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Add + RMSNorm of one row by the 256 threads of a workgroup (every thread
-// calls it; it synchronises the workgroup): h = x (+ res) in fp32,
+// Add + RMSNorm of one row by the first 256 threads of a workgroup (every
+// thread calls it; it synchronises the workgroup; threads past 256 hold no
+// elements, so a larger workgroup gives the same bits): h = x (+ res) in fp32,
 // out = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * w), res_out = bf16(h) (when
 // res_out). Thread t holds the 8-element chunks t, t + 256, ... (H <= 8192,
 // H % 8 == 0); the sum of squares runs per thread over its chunks, then over
@@ -142,7 +143,7 @@ __device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
     const int e0 = (c * 256 + static_cast<int>(threadIdx.x)) * 8;
-    if (e0 < H) {
+    if (threadIdx.x < 256 && e0 < H) {
       const u32x4 a = load16(x + e0);
       const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
       u32x4 b = {0u, 0u, 0u, 0u};
@@ -160,7 +161,7 @@ __device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (lane == 0) red[wave] = ss;
+  if (lane == 0 && wave < 4) red[wave] = ss;
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
@@ -170,7 +171,7 @@ __device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
     const int e0 = (c * 256 + static_cast<int>(threadIdx.x)) * 8;
-    if (e0 < H) {
+    if (threadIdx.x < 256 && e0 < H) {
       const u32x4 wv = load16(w + e0);
       const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
       uint32_t o[4], ro[4];

@@ -148,22 +148,23 @@ template <> __device__ __forceinline__ u32x4 dequant8<__bf16>(uint32_t w0, uint3
 // (sd::add_rmsnorm_row, the RMSNorm kernel's own arithmetic), formed while
 // staging; workgroup x = 0 of each activation block writes the new residual.
 template <typename T, int MT, int NT, int KW, int U, bool PER_GROUP, bool CONTIG = false,
-          int D = 2, bool XL = false, int MODE = 0>
-__global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
+          int D = 2, bool XL = false, int MODE = 0, int NWV = kWaves>
+__global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
   constexpr bool SL = MODE == 1;
   constexpr bool NM = MODE == 2;
+  constexpr int NTH = NWV * 64;  // threads of the workgroup
   static_assert(!NM || XL, "the norm is formed while staging");
   static_assert(U == 2 || U == 4 || U == 8, "a chunk row segment is 64 U bytes");
   constexpr int LPR = 4 * U;         // lanes per row segment (16-byte units per row)
   constexpr int RPI = 64 / LPR;      // row segments per load instruction
   constexpr int NLD = 16 * NT / RPI; // load instructions per chunk
-  constexpr int NSUB = kWaves / KW;  // row groups a workgroup works on at once
+  constexpr int NSUB = NWV / KW;  // row groups a workgroup works on at once
   constexpr int SWZ = (LPR < 16 ? LPR : 16) - 1;  // position swizzle stays inside a row
   // DIRECT: each lane loads its own A operand (row l % 16, 16 bytes at
   // k = 64 step + 16 (l / 16)) straight from HBM, no LDS tile
   constexpr bool DIRECT = XL && MT >= 2;
   constexpr int TILE = DIRECT ? 16 : 16 * NT * LPR * 16;  // bytes of one wave's LDS tile
-  __shared__ __attribute__((aligned(16))) char wtile[kWaves][TILE];
+  __shared__ __attribute__((aligned(16))) char wtile[NWV][TILE];
   __shared__ __attribute__((aligned(16))) float red[KW > 1 ? KW - 1 : 1][NT * MT * 4][64];
   extern __shared__ __attribute__((aligned(16))) char xsm[];  // XL: activation rows
 
@@ -382,14 +383,16 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
       }
       __syncthreads();
       if (kw == 0) {
+        // partials added in wave order (a few slots per pass: with 16 waves,
+        // all 60 in flight would not fit the registers of a 1024-thread group)
+#pragma unroll 3
+        for (int w = 0; w < KW - 1; ++w)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
+          for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-              for (int w = 0; w < KW - 1; ++w) acc[nt][mt][i] += red[w][(nt * MT + mt) * 4 + i][lane];
+              for (int i = 0; i < 4; ++i) acc[nt][mt][i] += red[w][(nt * MT + mt) * 4 + i][lane];
       }
     }
     if (kw == 0) {
@@ -457,13 +460,13 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
       // a few rows (decode), not for many.
       uint16_t* ro = p.nres && p.nres_out && blockIdx.x == 0 ? p.nres_out + m0 * p.nres_out_s : nullptr;
       const uint16_t* res = p.nres ? p.nres + m0 * p.nres_s : nullptr;
-      __shared__ float nred[kThreads / 64];
+      __shared__ float nred[4];
       for (int r = 0; r < rows; ++r)
         sd::add_rmsnorm_row<T>(p.x + (m0 + r) * p.xs, res ? res + r * p.nres_s : nullptr, p.nw, p.K,
                                p.neps, nred, reinterpret_cast<uint16_t*>(xsm + r * p.xpitch),
                                ro ? ro + r * p.nres_out_s : nullptr);
     } else {
-      for (int idx = tid; idx < rows * upr; idx += kThreads) {
+      for (int idx = tid; idx < rows * upr; idx += NTH) {
         const int r = idx / upr, c = idx - r * upr;
         const uint16_t* src = p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8;
         if constexpr (SL)
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
     }
     // scales (and bias) of the rows every wave of this workgroup owns
     const int per_sub = p.ngmax * RG;
-    for (int idx = tid; idx < NSUB * per_sub * spr; idx += kThreads) {
+    for (int idx = tid; idx < NSUB * per_sub * spr; idx += NTH) {
       const int j = idx % spr, t = idx / spr;
       const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
       const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
@@ -483,7 +486,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Params p) {
                             PER_GROUP ? static_cast<int64_t>(n) * spr + j : n);
     }
     if (p.bias) {
-      for (int t = tid; t < NSUB * per_sub; t += kThreads) {
+      for (int t = tid; t < NSUB * per_sub; t += NTH) {
         const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
         const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
         bis[t] = sd::from_bits<T>(p.bias[min(g * RG + r, p.N - 1)]);
@@ -773,21 +776,27 @@ W8Plan make_plan(int64_t M, int64_t N, int64_t K) {
   const int cus = sd::device_cus();
   const int64_t nks = K / 64;
   // Enough 16-row tiles for ~8 waves per CU: every wave owns whole rows, two
-  // tiles at a time. Otherwise four waves split K of one tile (16 activation
-  // rows: the measured best for the narrow layers at every M).
+  // tiles at a time. Otherwise KW waves of one workgroup split K of one tile
+  // (16 activation rows) and their partials meet in LDS in wave order: 16 or
+  // 8 when that keeps at most about 16 waves per CU busy with whole 2-step
+  // chunks each (a narrow layer has too few tiles to fill the GPU with 4:
+  // N = 1024 is 64 workgroups), else 4.
   if (nr * pl.mblocks >= 8ll * cus || nks < 4) {
     pl.KW = 1;
     // 16-row groups balance better over the waves (lm_head M = 1: 29.0 vs
     // 30.0 us); from M = 8 up, 32-row groups reuse each activation read twice
     pl.NT = nr < 2 || M <= 4 ? 1 : 2;
   } else {
-    pl.KW = 4;
     pl.NT = 1;
     pl.MT = 1;
     pl.mblocks = static_cast<int>((M + 15) / 16);
+    const int64_t tiles = nr * pl.mblocks;
+    // (whole 2-step chunks per wave: a partial chunk loads steps nobody uses)
+    pl.KW = tiles * 16 <= 16ll * cus && nks % 32 == 0 ? 16
+            : (tiles * 8 <= 16ll * cus && nks % 16 == 0 ? 8 : 4);
   }
   pl.groups = static_cast<int>((nr + pl.NT - 1) / pl.NT);
-  const int nsub = kWaves / pl.KW;
+  const int nsub = pl.KW > 1 ? 1 : kWaves;
   const int64_t need = (pl.groups + nsub - 1) / nsub;
   pl.grid = static_cast<int>(need < (1 << 30) ? need : (1 << 30));  // capped at launch
   return pl;
@@ -798,7 +807,7 @@ W8Plan make_plan(int64_t M, int64_t N, int64_t K) {
 // LDS on the current device, cached per (kernel, device, smem): every
 // instance of the kernel template has the same function type, so the key must
 // be the kernel's address.
-int resident_wgs_of(const void* kern, size_t smem) {
+int resident_wgs_of(const void* kern, size_t smem, int threads = kThreads) {
   struct Entry {
     const void* kern;
     int dev;
@@ -816,7 +825,7 @@ int resident_wgs_of(const void* kern, size_t smem) {
       if (table[i].kern == kern && table[i].dev == dev && table[i].smem == smem) return table[i].n;
   }
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, smem) != hipSuccess || n <= 0)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, smem) != hipSuccess || n <= 0)
     n = 1;
   std::lock_guard<std::mutex> lock(mu);
   if (used < 512) table[used++] = Entry{kern, dev, smem, n};
@@ -824,8 +833,8 @@ int resident_wgs_of(const void* kern, size_t smem) {
 }
 
 template <typename Kern>
-int resident_wgs(Kern kern) {
-  return resident_wgs_of(reinterpret_cast<const void*>(kern), 0);
+int resident_wgs(Kern kern, int threads = kThreads) {
+  return resident_wgs_of(reinterpret_cast<const void*>(kern), 0, threads);
 }
 
 // Activation rows staged in LDS (XL): bytes per row pad and the most a
@@ -843,21 +852,26 @@ constexpr int kXlMaxBytesSplit = 16 * (1024 * 2 + kXPad);
 constexpr int kXlScaleBytes = 32 * 1024;
 
 template <typename Kern>
-int resident_wgs_xl(Kern kern, size_t smem) {
-  return resident_wgs_of(reinterpret_cast<const void*>(kern), smem);
+int resident_wgs_xl(Kern kern, size_t smem, int threads = kThreads) {
+  return resident_wgs_of(reinterpret_cast<const void*>(kern), smem, threads);
 }
 
 // Static LDS of w8a16_kernel<.., MT, NT, KW, U, ..>: the weight tiles and the
 // K-split reduction slot, as the kernel declares them.
-template <int MT, int NT, int KW, int U, bool XL>
+template <int MT, int NT, int KW, int U, bool XL, int NWV = kWaves>
 constexpr size_t w8_static_lds() {
-  return static_cast<size_t>(kWaves) * (XL && MT >= 2 ? 16 : 16 * NT * 4 * U * 16) +
+  return static_cast<size_t>(NWV) * (XL && MT >= 2 ? 16 : 16 * NT * 4 * U * 16) +
          static_cast<size_t>(KW > 1 ? KW - 1 : 1) * (NT * MT * 4) * 64 * 4;
 }
 
 template <typename T, int MT, int NT, int KW, bool PG, int MODE>
 int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
-  constexpr int U = NT >= 2 ? 2 : 4;  // 64-k steps per chunk
+  // 64-k steps per chunk: 2 where a wave's K slice is a few steps (8 or 16
+  // slices) or the chunk covers 32 rows
+  constexpr int U = NT >= 2 || KW >= 8 ? 2 : 4;
+  // K-split workgroups have one wave per K slice; whole-row ones four waves
+  constexpr int NWV = KW > 1 ? KW : kWaves;
+  constexpr int NTH = NWV * 64;
   {
     // activation rows staged in LDS (XL): wide layers up to kXlMaxBytes (their
     // occupancy matters); K-split kernels as kXlMaxBytesSplit says
@@ -872,11 +886,11 @@ int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
       // M = 56, two 32-row blocks before the loads were pipelined: 63.8 us;
       // 8-step chunks through the tile at one workgroup per CU: 77.8 us)
       constexpr int UX = MT >= 2 ? 2 : U;
-      constexpr int NSUB = kWaves / KW;
-      auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true, MODE>;
+      constexpr int NSUB = NWV / KW;
+      auto kern = w8a16_kernel<T, MT, NT, KW, UX, PG, false, 2, true, MODE, NWV>;
       // occupancy from the activation rows; the scale table adds a few KB (per
       // channel: 16 B per row of the workgroup)
-      unsigned cap = static_cast<unsigned>(sd::device_cus() * resident_wgs_xl(kern, xbytes)) /
+      unsigned cap = static_cast<unsigned>(sd::device_cus() * resident_wgs_xl(kern, xbytes, NTH)) /
                      grid.y;
       cap = cap >= 8 ? cap / 8 * 8 : 1;
       if (grid.x > cap) grid.x = cap;
@@ -885,10 +899,10 @@ int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
       q.ngmax = (p.groups + static_cast<int>(grid.x) * NSUB - 1) / (static_cast<int>(grid.x) * NSUB);
       const size_t spr = PG ? static_cast<size_t>(p.K / p.group) : 1;
       const size_t tbl = static_cast<size_t>(NSUB) * q.ngmax * NT * 16 * (spr + (p.bias ? 1 : 0)) * 4;
-      const size_t lds = w8_static_lds<MT, NT, KW, UX, true>() + q.xbytes + tbl;
+      const size_t lds = w8_static_lds<MT, NT, KW, UX, true, NWV>() + q.xbytes + tbl;
       if (tbl <= static_cast<size_t>(kXlScaleBytes) &&
           lds <= static_cast<size_t>(sd::device_lds_per_block())) {
-        hipLaunchKernelGGL(kern, grid, dim3(kThreads), q.xbytes + tbl, st, q);
+        hipLaunchKernelGGL(kern, grid, dim3(NTH), q.xbytes + tbl, st, q);
         return SD_OK;
       }
     }
@@ -899,14 +913,14 @@ int launch_k(const W8Params& p, dim3 grid, hipStream_t st) {
                   "staging LDS", static_cast<int>(p.M < MT * 16 ? p.M : MT * 16), p.K);
     return SD_ERR_UNSUPPORTED;
   } else {
-    auto kern = w8a16_kernel<T, MT, NT, KW, U, PG, false, 2, false, MODE>;
+    auto kern = w8a16_kernel<T, MT, NT, KW, U, PG, false, 2, false, MODE, NWV>;
     // exactly one resident set of workgroups over all activation blocks (a
     // partial second round would leave most of the GPU idle at the end), grid.x
     // a multiple of 8 so that block (x, y) shares an XCD (and its L2) with (x, 0)
-    unsigned cap = static_cast<unsigned>(sd::device_cus() * resident_wgs(kern)) / grid.y;
+    unsigned cap = static_cast<unsigned>(sd::device_cus() * resident_wgs(kern, NTH)) / grid.y;
     cap = cap >= 8 ? cap / 8 * 8 : 1;
     if (grid.x > cap) grid.x = cap;
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL(kern, grid, dim3(NTH), 0, st, p);
     return SD_OK;
   }
 }
@@ -931,11 +945,19 @@ int launch_all(const W8Params& p, const W8Plan& pl, hipStream_t st) {
   int rc;
   const dim3 grid(static_cast<unsigned>(pl.grid), static_cast<unsigned>(pl.mblocks));
   if (p.group == 0) {
-    if (pl.KW == 1) rc = launch_kw<T, false, 1, MODE>(p, pl, grid, st);
-    else rc = launch_kw<T, false, 4, MODE>(p, pl, grid, st);
+    switch (pl.KW) {
+      case 1: rc = launch_kw<T, false, 1, MODE>(p, pl, grid, st); break;
+      case 16: rc = launch_kw<T, false, 16, MODE>(p, pl, grid, st); break;
+      case 8: rc = launch_kw<T, false, 8, MODE>(p, pl, grid, st); break;
+      default: rc = launch_kw<T, false, 4, MODE>(p, pl, grid, st); break;
+    }
   } else {
-    if (pl.KW == 1) rc = launch_kw<T, true, 1, MODE>(p, pl, grid, st);
-    else rc = launch_kw<T, true, 4, MODE>(p, pl, grid, st);
+    switch (pl.KW) {
+      case 1: rc = launch_kw<T, true, 1, MODE>(p, pl, grid, st); break;
+      case 16: rc = launch_kw<T, true, 16, MODE>(p, pl, grid, st); break;
+      case 8: rc = launch_kw<T, true, 8, MODE>(p, pl, grid, st); break;
+      default: rc = launch_kw<T, true, 4, MODE>(p, pl, grid, st); break;
+    }
   }
   if (rc != SD_OK) return rc;
   return sd::check_launch("w8a16");
