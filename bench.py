@@ -51,6 +51,9 @@ def parse():
     ap.add_argument("--no-draft-chain", action="store_true",
                     help="skip the C5 draft-chain extra (its thousands of launches swamp a trace)")
     ap.add_argument("--profile-pass", action="store_true")
+    ap.add_argument("--draft-chain-only", type=int, default=0, metavar="B",
+                    help="only the fused C5 draft chain at batch B, replayed a few times "
+                         "(for a kernel trace); prints us per draft step")
     return ap.parse_args()
 
 
@@ -528,6 +531,16 @@ def main():
         sys.exit(1)
     if args.profile_pass:
         profile_pass(ops, workloads, torch)
+        return
+    if args.draft_chain_only:
+        from specdec_nanovllm_amd.draft_chain import DraftChain
+        ch = DraftChain(args.draft_chain_only, ctx_len=2048, k=6, seed=args.draft_chain_only,
+                        fused=True)
+        g = graph_of(ch.chain, torch)
+        step = time_replays([g], 5, 1, torch) * 1e3 / ch.k
+        print(json.dumps({"draft_chain_only": args.draft_chain_only, "fused": True,
+                          "step_us": round(step, 2), "replays": 6, "steps_per_replay": ch.k}),
+              flush=True)
         return
 
     B = args.batch

@@ -190,6 +190,76 @@ __device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_
   }
 }
 
+// add_rmsnorm_row by one wave, in two passes over the row (sum of squares,
+// then the outputs), with the same bits: the wave plays the 4 waves of the
+// 256-thread form one after another (virtual thread 64 vw + lane holds the
+// chunks c * 256 + 64 vw + lane, c = 0..3), adds each virtual wave's squares
+// with the same xor steps, and the 4 wave sums in order. No LDS and no
+// workgroup barrier, so the waves of a workgroup can normalise different rows
+// at the same time.
+template <typename T>
+__device__ __forceinline__ void add_rmsnorm_row_wave(const uint16_t* x, const uint16_t* res,
+                                                     const uint16_t* w, int H, float eps,
+                                                     uint16_t* out, uint16_t* res_out) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  auto row_val = [&](const u32x4& a, const u32x4& b, int i) {
+    const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+    float f = from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
+    if (res) f = f + from_bits<T>(static_cast<uint16_t>(bw[i / 2] >> (16 * (i & 1))));
+    return f;
+  };
+  float tot = 0.f;
+#pragma unroll
+  for (int vw = 0; vw < 4; ++vw) {
+    if (vw * 64 * 8 >= H) break;  // wave-uniform: no chunk of this virtual wave is in the row
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int e0 = (c * 256 + vw * 64 + lane) * 8;
+      if (e0 < H) {
+        const u32x4 a = load16(x + e0);
+        const u32x4 b = res ? load16(res + e0) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float f = row_val(a, b, i);
+          ss += f * f;
+        }
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    tot += ss;
+  }
+  const float r = rsqrtf(tot / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int vw = 0; vw < 4; ++vw) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int e0 = (c * 256 + vw * 64 + lane) * 8;
+      if (e0 < H) {
+        const u32x4 a = load16(x + e0);
+        const u32x4 b = res ? load16(res + e0) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 wv = load16(w + e0);
+        const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+        uint32_t o[4], ro[4];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          const float v0 = row_val(a, b, i), v1 = row_val(a, b, i + 1);
+          const float w0 = from_bits<T>(static_cast<uint16_t>(ww[i / 2]));
+          const float w1 = from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> 16));
+          const float n0 = static_cast<float>(static_cast<T>(v0 * r));
+          const float n1 = static_cast<float>(static_cast<T>(v1 * r));
+          o[i / 2] = pack2<T>(n0 * w0, n1 * w1);
+          ro[i / 2] = pack2<T>(v0, v1);
+        }
+        store16(out + e0, u32x4{o[0], o[1], o[2], o[3]});
+        if (res_out) store16(res_out + e0, u32x4{ro[0], ro[1], ro[2], ro[3]});
+      }
+    }
+  }
+}
+
 // SiluAndMul on 8 elements: bf16(bf16(silu(g)) * u) per element (T = the
 // activation type), the eager module's roundings; g and u are 8 packed 16-bit
 // values each. Shared by the SiLU kernel and the W8A16 activation path that

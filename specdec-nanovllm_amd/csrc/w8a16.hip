@@ -145,8 +145,9 @@ template <> __device__ __forceinline__ u32x4 dequant8<__bf16>(uint32_t w0, uint3
 // the activation is loaded (the down projection reads the gate_up projection's
 // output directly).
 // MODE 2 (NM, staged only): the activation is the add + RMSNorm of the rows
-// (sd::add_rmsnorm_row, the RMSNorm kernel's own arithmetic), formed while
-// staging; workgroup x = 0 of each activation block writes the new residual.
+// (sd::add_rmsnorm_row_wave: one wave per row, the RMSNorm kernel's own
+// arithmetic and summation order), formed while staging; workgroup x = 0 of
+// each activation block writes the new residual.
 template <typename T, int MT, int NT, int KW, int U, bool PER_GROUP, bool CONTIG = false,
           int D = 2, bool XL = false, int MODE = 0, int NWV = kWaves>
 __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
@@ -454,17 +455,15 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
     const int rows = min(MT * 16, p.M - m0);
     const int upr = p.K / 8;  // 16-byte units per row
     if constexpr (NM) {
-      // rows one after another, each by the whole workgroup (the registers hold
-      // it between the two passes); one workgroup per row block writes the
-      // residual sum. Every workgroup repeats this for its block: it pays for
-      // a few rows (decode), not for many.
+      // one wave per row, the waves' rows at the same time (the RMSNorm
+      // kernel's bits, sd::add_rmsnorm_row_wave); one workgroup per row block
+      // writes the residual sum. Every workgroup repeats this for its block.
       uint16_t* ro = p.nres && p.nres_out && blockIdx.x == 0 ? p.nres_out + m0 * p.nres_out_s : nullptr;
       const uint16_t* res = p.nres ? p.nres + m0 * p.nres_s : nullptr;
-      __shared__ float nred[4];
-      for (int r = 0; r < rows; ++r)
-        sd::add_rmsnorm_row<T>(p.x + (m0 + r) * p.xs, res ? res + r * p.nres_s : nullptr, p.nw, p.K,
-                               p.neps, nred, reinterpret_cast<uint16_t*>(xsm + r * p.xpitch),
-                               ro ? ro + r * p.nres_out_s : nullptr);
+      for (int r = wave; r < rows; r += NWV)
+        sd::add_rmsnorm_row_wave<T>(p.x + (m0 + r) * p.xs, res ? res + r * p.nres_s : nullptr, p.nw,
+                                    p.K, p.neps, reinterpret_cast<uint16_t*>(xsm + r * p.xpitch),
+                                    ro ? ro + r * p.nres_out_s : nullptr);
     } else {
       for (int idx = tid; idx < rows * upr; idx += NTH) {
         const int r = idx / upr, c = idx - r * upr;
