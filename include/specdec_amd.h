@@ -340,13 +340,15 @@ int sd_w8a16_rmsnorm_linear(const void* x, int64_t x_stride_m, const void* resid
  * The layer's post_attention_layernorm, gate_up_proj and act_fn
  * (models/qwen3.py Qwen3MLP.forward, layers/activation.py:6-11) in one launch;
  * no counterpart entry in the reference. y equals sd_w8a16_rmsnorm_linear (or
- * sd_w8a16_linear) followed by sd_silu_mul bit for bit. A wave streams gate
- * row i together with up row I + i and forms the SiLU of the pair once, so
- * the down projection reads the activated rows with no SiLU of its own.
- * Row-streaming path only: one or two rows, M * ceil(K / 1024) <= 4,
- * per-channel scale, at most 32 MiB of weights, N even; other shapes return
- * SD_ERR_UNSUPPORTED (the caller runs the two calls). y: (M, N / 2) dtype,
- * sharing no byte with x, residual or residual_out.
+ * sd_w8a16_linear) followed by sd_silu_mul bit for bit. On the row-streaming
+ * path (one or two rows, M * ceil(K / 1024) <= 4, per-channel scale, at most
+ * 32 MiB of weights, N even) a wave streams gate row i together with up row
+ * I + i; on the K-split path of sd_w8a16_linear (narrow layers, per-channel
+ * scale, N a multiple of 32) a workgroup takes gate tile g and up tile g with
+ * the plain projection's K split, so the sums are the projection's own. The
+ * down projection then reads the activated rows with no SiLU of its own.
+ * Other shapes return SD_ERR_UNSUPPORTED (the caller runs the two calls).
+ * y: (M, N / 2) dtype, sharing no byte with x, residual or residual_out.
  */
 int sd_w8a16_gate_up_silu(const void* x, int64_t x_stride_m, const void* residual,
                           int64_t residual_stride_m, void* residual_out,

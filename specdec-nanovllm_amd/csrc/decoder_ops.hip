@@ -31,7 +31,7 @@ template <typename T> __device__ __forceinline__ float ld(const uint16_t* p, int
   return sd::from_bits<T>(p[i]);
 }
 template <typename T> __device__ __forceinline__ float round16(float x) {
-  return static_cast<float>(static_cast<T>(x));
+  return static_cast<float>(sd::round16<T>(x));
 }
 
 // Block-wide fp32 sum (every thread gets it). `red` holds kThreads / 64 floats.

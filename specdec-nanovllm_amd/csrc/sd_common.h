@@ -41,9 +41,19 @@ template <> struct Elem<_Float16> {
   }
 };
 
+// fp32 -> T, round to nearest even, of the fp32 value itself. The empty asm
+// keeps the compiler from folding the multiply-add that produced x into the
+// conversion (v_fma_mix*_f16 rounds the exact a * b + c straight to fp16, one
+// rounding where the source says two): without it the bits of an fp16 output
+// near a rounding midpoint depend on which form the compiler picked for that
+// output, so two kernels computing the same fp32 value could disagree.
+template <typename T> __device__ __forceinline__ T round16(float x) {
+  asm("" : "+v"(x));
+  return static_cast<T>(x);
+}
 // fp32 -> 16-bit storage bits, round to nearest even.
 template <typename T> __device__ __forceinline__ uint16_t to_bits(float x) {
-  return __builtin_bit_cast(uint16_t, static_cast<T>(x));
+  return __builtin_bit_cast(uint16_t, round16<T>(x));
 }
 // Pack two fp32 into one dword of two 16-bit values (lo in bits 0..15).
 template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
@@ -56,7 +66,7 @@ template <typename T> __device__ __forceinline__ float from_bits(uint16_t b) {
 // a = float(hi_a) + float(lo_a) to ~2^-17 relative (hi and lo each RNE).
 template <typename T>
 __device__ __forceinline__ void split_pack(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const T ha = static_cast<T>(a), hb = static_cast<T>(b);
+  const T ha = round16<T>(a), hb = round16<T>(b);
   hi = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
   lo = pack2<T>(a - static_cast<float>(ha), b - static_cast<float>(hb));
@@ -179,8 +189,8 @@ __device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_
       for (int i = 0; i < 8; i += 2) {
         const float w0 = from_bits<T>(static_cast<uint16_t>(ww[i / 2]));
         const float w1 = from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> 16));
-        const float n0 = static_cast<float>(static_cast<T>(v[c][i] * r));
-        const float n1 = static_cast<float>(static_cast<T>(v[c][i + 1] * r));
+        const float n0 = static_cast<float>(round16<T>(v[c][i] * r));
+        const float n1 = static_cast<float>(round16<T>(v[c][i + 1] * r));
         o[i / 2] = pack2<T>(n0 * w0, n1 * w1);
         ro[i / 2] = pack2<T>(v[c][i], v[c][i + 1]);
       }
@@ -248,8 +258,8 @@ __device__ __forceinline__ void add_rmsnorm_row_wave(const uint16_t* x, const ui
           const float v0 = row_val(a, b, i), v1 = row_val(a, b, i + 1);
           const float w0 = from_bits<T>(static_cast<uint16_t>(ww[i / 2]));
           const float w1 = from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> 16));
-          const float n0 = static_cast<float>(static_cast<T>(v0 * r));
-          const float n1 = static_cast<float>(static_cast<T>(v1 * r));
+          const float n0 = static_cast<float>(round16<T>(v0 * r));
+          const float n1 = static_cast<float>(round16<T>(v1 * r));
           o[i / 2] = pack2<T>(n0 * w0, n1 * w1);
           ro[i / 2] = pack2<T>(v0, v1);
         }
@@ -268,7 +278,7 @@ __device__ __forceinline__ void add_rmsnorm_row_wave(const uint16_t* x, const ui
 template <typename T>
 __device__ __forceinline__ float silu_mul1(float gv, float uv) {
 #pragma clang fp contract(off)
-  const float sv = static_cast<float>(static_cast<T>(gv / (1.f + expf(-gv))));
+  const float sv = static_cast<float>(round16<T>(gv / (1.f + expf(-gv))));
   return sv * uv;
 }
 

@@ -209,6 +209,15 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
   auto srow = [&](int g, int r) {  // scale-table row of row r of group g (this wave's)
     return (sub * p.ngmax + (g - g0) / gstride) * RG + r;
   };
+  // pr: gate_up with the SiLU epilogue on the K-split path. Group g is gate tile
+  // g (weight rows 16 g ..) and up tile g (rows pair + 16 g ..); its 16 outputs
+  // are bf16(bf16(silu(gate)) * up) of the rows the projection would write.
+  constexpr bool PRC = KW > 1 && NT == 2 && MODE != 1 && !PER_GROUP;
+  const bool pr = PRC && p.pair > 0;
+  const int nrows = pr ? 2 * p.pair : p.N;  // weight rows
+  auto wrow = [&](int g, int r) {  // weight row of row r (0 .. RG - 1) of group g
+    return pr ? (r < 16 ? g * 16 + r : p.pair + g * 16 + (r - 16)) : g * RG + r;
+  };
 
   // Activation rows past M are never loaded: those lanes keep zeros (only the
   // lanes of real rows touch memory, e.g. 4 of 64 at M = 1).
@@ -255,7 +264,7 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
     (void)kw_off;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const int n = min(n0 + nt * 16 + lr, p.N - 1);
+      const int n = min(wrow(g, nt * 16 + lr), nrows - 1);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t ko = static_cast<int64_t>(min(s0 + u, p.nks - 1)) * 64 + lg * 16;
@@ -265,7 +274,7 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
     } else {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int n = min(n0 + i * RPI + ld_row, p.N - 1);
+      const int n = min(wrow(g, i * RPI + ld_row), nrows - 1);
       R.w[i] = sd::load16_stream(p.w + sd::keep_or_zero(real, static_cast<int64_t>(n) * p.ws + kw_off));
     }
     }
@@ -396,7 +405,48 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
               for (int i = 0; i < 4; ++i) acc[nt][mt][i] += red[w][(nt * MT + mt) * 4 + i][lane];
       }
     }
-    if (kw == 0) {
+    bool paired = false;
+    if constexpr (PRC) {
+      if (kw == 0 && pr) {
+        paired = true;
+        const int nb = g * 16 + lg * 4;  // output column (pair) of this lane's 4 sums
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = m0 + mt * 16 + lr;
+          if (m >= p.M || nb >= p.N) continue;
+          float o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {  // gate, up: the projection's rounded output
+              const int r = h * 16 + lg * 4 + i;
+              float sc, bi;
+              if constexpr (XL) {
+                sc = scl[srow(g, r)];
+                bi = p.bias ? bis[srow(g, r)] : 0.f;
+              } else {
+                const int n = wrow(g, r);
+                sc = load_scale(p.scale, p.scale_dtype, n);
+                bi = p.bias ? sd::from_bits<T>(p.bias[n]) : 0.f;
+              }
+              v[h] = sd::from_bits<T>(sd::to_bits<T>(acc[h][mt][i] * sc + bi));
+            }
+            o[i] = sd::silu_mul1<T>(v[0], v[1]);
+          }
+          uint16_t* dst = p.y + static_cast<int64_t>(m) * p.ys + nb;
+          if (nb + 3 < p.N && (reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(sd::pack2<T>(o[0], o[1]), sd::pack2<T>(o[2], o[3]));
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (nb + i < p.N) dst[i] = sd::to_bits<T>(o[i]);
+          }
+        }
+      }
+    }
+    if (kw == 0 && !paired) {
       const int n0 = g * NT * 16;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -480,7 +530,7 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
       const int j = idx % spr, t = idx / spr;
       const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
       const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
-      const int n = min(g * RG + r, p.N - 1);
+      const int n = min(wrow(g, r), nrows - 1);
       scl[idx] = load_scale(p.scale, p.scale_dtype,
                             PER_GROUP ? static_cast<int64_t>(n) * spr + j : n);
     }
@@ -488,7 +538,7 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
       for (int t = tid; t < NSUB * per_sub; t += NTH) {
         const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
         const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
-        bis[t] = sd::from_bits<T>(p.bias[min(g * RG + r, p.N - 1)]);
+        bis[t] = sd::from_bits<T>(p.bias[min(wrow(g, r), nrows - 1)]);
       }
     }
     __syncthreads();
@@ -637,9 +687,9 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
             const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-              const float n = static_cast<float>(static_cast<T>(xv[m][c][8 * e + i] * rn));
+              const float n = static_cast<float>(sd::round16<T>(xv[m][c][8 * e + i] * rn));
               const float wv = sd::from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> (16 * (i & 1))));
-              xv[m][c][8 * e + i] = static_cast<float>(static_cast<T>(n * wv));
+              xv[m][c][8 * e + i] = static_cast<float>(sd::round16<T>(n * wv));
             }
           }
         }
@@ -935,6 +985,10 @@ int launch_kw(const W8Params& p, const W8Plan& pl, dim3 grid, hipStream_t st) {
       default: return launch_k<T, 2, 2, 1, PG, MODE>(p, grid, st);
     }
   } else {
+    if (p.pair > 0) {  // gate_up with the SiLU epilogue: gate and up tile per group
+      if constexpr (!PG && MODE != 1) return launch_k<T, 1, 2, KW, PG, MODE>(p, grid, st);
+      else return SD_ERR_UNSUPPORTED;
+    }
     return launch_k<T, 1, 1, KW, PG, MODE>(p, grid, st);  // make_plan sets MT = 1 with KW > 1
   }
 }
@@ -1147,17 +1201,36 @@ int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& nor
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int mode = up >= 0 ? 1 : (p.nw ? 2 : 0);
   if (pair) {
-    if (N % 2 != 0 || !rows_eligible(p)) {
+    // the row-streaming path (one or two rows), or the K-split tiled path with
+    // the plain projection's plan (same K split, so the same sums), per-channel
+    // scales and whole 16-row tiles of pairs
+    const bool rows = N % 2 == 0 && rows_eligible(p);
+    const bool tiled = N % 32 == 0 && pl.KW > 1 && group_size == 0 && mode != 1;
+    if (!rows && !tiled) {
       sd::set_error("w8a16_gate_up_silu: the SiLU epilogue runs on the row-streaming path "
                     "(one or two rows, M * ceil(K / 1024) <= 4, per-channel scales, at most "
-                    "32 MiB of weights, N even); got M=%lld N=%lld K=%lld group=%d",
+                    "32 MiB of weights, N even) or on the K-split path (narrow layers, "
+                    "per-channel scales, N a multiple of 32); got M=%lld N=%lld K=%lld group=%d",
                     (long long)M, (long long)N, (long long)K, group_size);
       return SD_ERR_UNSUPPORTED;
     }
     p.pair = static_cast<int32_t>(N / 2);
     p.N = static_cast<int32_t>(N / 2);
-    if (dtype == SD_BF16) return launch_rows_any<__bf16>(p, mode, st);
-    return launch_rows_any<_Float16>(p, mode, st);
+    if (rows) {
+      if (dtype == SD_BF16) return launch_rows_any<__bf16>(p, mode, st);
+      return launch_rows_any<_Float16>(p, mode, st);
+    }
+    W8Plan pp = pl;
+    pp.NT = 2;
+    pp.groups = static_cast<int>(N / 32);
+    pp.grid = pp.groups;
+    p.groups = pp.groups;
+    if (mode == 2) {
+      if (dtype == SD_BF16) return launch_all<__bf16, 2>(p, pp, st);
+      return launch_all<_Float16, 2>(p, pp, st);
+    }
+    if (dtype == SD_BF16) return launch_all<__bf16, 0>(p, pp, st);
+    return launch_all<_Float16, 0>(p, pp, st);
   }
   if (rows_eligible(p)) {
     if (dtype == SD_BF16) return launch_rows_any<__bf16>(p, mode, st);

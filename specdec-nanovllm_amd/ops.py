@@ -448,8 +448,11 @@ def w8a16_gate_up_silu(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tens
     (``residual_out`` as in ``w8a16_rmsnorm_linear``). qweight (2I, K) =
     [gate; up], per-channel scale (2I,); returns (..., I), bit for bit the
     separate calls. One launch on the row-streaming path (one or two rows,
-    weights up to 32 MiB): a wave streams gate row i with up row I + i and
-    forms the pair's SiLU once; other shapes take the separate launches."""
+    weights up to 32 MiB: a wave streams gate row i with up row I + i and
+    forms the pair's SiLU once) and on the K-split path of narrow layers (a
+    workgroup takes gate tile g and up tile g with the plain projection's K
+    split; with the norm, above 4 rows, the RMSNorm launch comes first);
+    other shapes take the separate launches."""
     assert qweight.dtype == torch.int8 and qweight.dim() == 2
     N, K = qweight.shape
     assert N % 2 == 0 and x.shape[-1] == K
@@ -480,16 +483,31 @@ def w8a16_gate_up_silu(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tens
     if M == 0:
         return y.view(shape)
     lib = _lib.load()
+    xa, ra, roa, nwa = x2, r2, ro, nw
+    if nw is not None and M > 4 and K % 8 == 0 and K <= 8192:
+        # the staged norm pays at up to 4 rows (every workgroup normalises all of
+        # them): the RMSNorm launch (writing residual_out itself), then the
+        # paired projection on the normalised rows
+        xa = torch.empty_like(x2)
+        rsum = ro if ro is not None or r2 is None else torch.empty_like(r2)
+        with torch.cuda.device(dev):
+            rc = lib.sd_rmsnorm(x2.data_ptr(), x2.stride(0), _ptr(r2),
+                                0 if r2 is None else r2.stride(0), nw.data_ptr(), xa.data_ptr(),
+                                xa.stride(0), _ptr(rsum), 0 if rsum is None else rsum.stride(0), M,
+                                K, float(eps), _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
+        _lib.check(rc)
+        ra = roa = nwa = None
     with torch.cuda.device(dev):
         rc = lib.sd_w8a16_gate_up_silu(
-            x2.data_ptr(), x2.stride(0), _ptr(r2), 0 if r2 is None else r2.stride(0),
-            _ptr(ro), 0 if ro is None else ro.stride(0), _ptr(nw), float(eps),
+            xa.data_ptr(), xa.stride(0), _ptr(ra), 0 if ra is None else ra.stride(0),
+            _ptr(roa), 0 if roa is None else roa.stride(0), _ptr(nwa), float(eps),
             qw.data_ptr(), qw.stride(0), sc.data_ptr(), _lib.dtype_code(sc.dtype), _ptr(b),
             y.data_ptr(), y.stride(0), M, N, K, _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
-    if rc == _lib.SD_ERR_UNSUPPORTED and (nw is None or (K % 8 == 0 and K <= 8192)):
-        # not on the row-streaming path: the projection, then the SiLU launch
-        if nw is None:
-            gu = w8a16_linear(x2, qw, sc, b)
+    if rc == _lib.SD_ERR_UNSUPPORTED and (nwa is None or (K % 8 == 0 and K <= 8192)):
+        # neither the row-streaming nor the K-split path: the projection, then
+        # the SiLU launch
+        if nwa is None:
+            gu = w8a16_linear(xa, qw, sc, b)
         else:
             gu = w8a16_rmsnorm_linear(x2, nw, eps, qw, sc, b, residual=r2, residual_out=ro)
         silu_mul(gu, out=y)

@@ -303,17 +303,24 @@ def test_row_streaming_path(M, K, gs, act):
                                                 (1, 8192, 4096, torch.bfloat16, True, True),
                                                 (1, 272, 1024, torch.bfloat16, True, True),
                                                 (3, 6144, 1024, torch.bfloat16, True, True),
-                                                (16, 6144, 1024, torch.float16, True, True)])
+                                                (4, 6144, 1024, torch.bfloat16, True, False),
+                                                (7, 6144, 1024, torch.bfloat16, False, False),
+                                                (16, 6144, 1024, torch.float16, True, True),
+                                                (16, 2048, 2048, torch.bfloat16, True, True),
+                                                (56, 6144, 1024, torch.float16, False, False),
+                                                (56, 6144, 1024, torch.bfloat16, True, True),
+                                                (5, 2064, 1024, torch.bfloat16, False, False)])
 def test_gate_up_silu_is_linear_then_silu_mul(M, N, K, act, norm, res):
     """The gate_up projection with the SiLU epilogue (paired gate / up rows on
-    the row-streaming path; the separate launches past it) equals the
+    the row-streaming path, paired gate / up tiles on the K-split path with the
+    plain projection's K split; the separate launches past them) equals the
     projection (with its RMSNorm) followed by the SiLU kernel, bit for bit."""
     c = workloads.w8a16_case(M, N, K, seed=M * 7 + N, act_dtype=act)
     g = workloads.device_generator(DEV, 31)
     x = (torch.randn((M, K), generator=g, device=DEV) * 2).to(act)
     r = torch.randn((M, K), generator=g, device=DEV).to(act) if res else None
     nw = (1 + 0.1 * torch.randn((K,), generator=g, device=DEV)).to(act) if norm else None
-    bias = torch.randn((N,), generator=g, device=DEV).to(act) if M == 2 else None
+    bias = torch.randn((N,), generator=g, device=DEV).to(act) if M in (2, 7, 56) else None
     if norm:
         ro_two = torch.empty_like(x) if res else None
         gu = ops.w8a16_rmsnorm_linear(x, nw, 1e-6, c["w"], c["s"], bias, residual=r,
@@ -330,12 +337,13 @@ def test_gate_up_silu_is_linear_then_silu_mul(M, N, K, act, norm, res):
         assert torch.equal(ro, ro_two)
 
 
-def test_gate_up_silu_entry_refuses_shapes_off_the_row_path():
-    c = workloads.w8a16_case(3, 2048, 1024, seed=5)
-    y = torch.empty((3, 1024), dtype=torch.float16, device=DEV)
+def test_gate_up_silu_entry_refuses_shapes_off_its_paths():
+    # 3 rows (not the row path) of 2064 weight rows (pairs not in whole 16-row tiles)
+    c = workloads.w8a16_case(3, 2064, 1024, seed=5)
+    y = torch.empty((3, 1032), dtype=torch.float16, device=DEV)
     lib = _lib.load()
     rc = lib.sd_w8a16_gate_up_silu(c["x"].data_ptr(), c["x"].stride(0), None, 0, None, 0, None,
                                    1e-6, c["w"].data_ptr(), c["w"].stride(0), c["s"].data_ptr(),
                                    _lib.dtype_code(c["s"].dtype), None, y.data_ptr(), y.stride(0),
-                                   3, 2048, 1024, _lib.SD_F16, _lib.stream_ptr(torch.device(DEV)))
+                                   3, 2064, 1024, _lib.SD_F16, _lib.stream_ptr(torch.device(DEV)))
     assert rc == _lib.SD_ERR_UNSUPPORTED and b"row-streaming" in lib.sd_last_error()
