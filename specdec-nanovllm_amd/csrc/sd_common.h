@@ -108,6 +108,13 @@ __device__ __forceinline__ int64_t keep_or_zero(bool keep, int64_t off) {
   return static_cast<int64_t>(static_cast<uint64_t>(off) & ((static_cast<uint64_t>(m) << 32) | m));
 }
 
+// keep_or_zero for a 32-bit offset.
+__device__ __forceinline__ uint32_t keep_or_zero32(bool keep, uint32_t off) {
+  uint32_t m = keep ? ~0u : 0u;
+  asm("" : "+v"(m));
+  return off & m;
+}
+
 // Orders LDS traffic between the lanes of one wave (a wave-private LDS tile
 // written by some lanes and read by others): a compiler barrier plus the
 // wavefront-scope fences of the AMDGPU memory model.

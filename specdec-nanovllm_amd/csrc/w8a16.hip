@@ -219,15 +219,15 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
     return pr ? (r < 16 ? g * 16 + r : p.pair + g * 16 + (r - 16)) : g * RG + r;
   };
 
-  // Activation rows past M are never loaded: those lanes keep zeros (only the
-  // lanes of real rows touch memory, e.g. 4 of 64 at M = 1). Staged blocks of
-  // 32 or 64 rows instead read the last staged row in their place, with no
-  // mask: an MFMA output column depends only on its own activation row, and
-  // the columns of rows past M are never written, while the zeros and the mask
-  // cost 9 VALU instructions per 16-row tile and step.
+  // Activation rows past M are never loaded from memory: those lanes keep
+  // zeros (only the lanes of real rows touch memory, e.g. 4 of 64 at M = 1).
+  // Staged rows (XL) are read from LDS with no mask, rows past M reading the
+  // last staged row: an MFMA output column depends only on its own activation
+  // row, and the columns of rows past M are never written, while the zeros and
+  // the mask cost 9 VALU instructions per 16-row tile and step.
   const uint16_t* xp[MT];
   bool xok[MT];
-  int xro[MT];  // XL, MT >= 2: LDS byte offset of the (clamped) staged row
+  int xro[MT];  // XL: LDS byte offset of the (clamped) staged row
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = m0 + mt * 16 + lr;
@@ -261,28 +261,30 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
   // prefetched after it.
   // `real` false (prefetch past the last item): every lane reads the same 16
   // bytes, one cache line instead of a re-read of streamed weight rows.
+  // Weight offsets are 32-bit from the scalar base p.w (the host checks that
+  // N x row stride < 4 GiB and the stride < 2^24): one 24-bit multiply-add
+  // per load instead of 64-bit address arithmetic.
+  const uint32_t ws32 = static_cast<uint32_t>(p.ws);
+  auto wload = [&](int n, uint32_t ko, bool real) {
+    return sd::load16_stream(p.w + sd::keep_or_zero32(real, __umul24(static_cast<uint32_t>(n), ws32) + ko));
+  };
   auto load = [&](Regs& R, int g, int c, bool real) {
-    const int n0 = g * NT * 16;
     const int s0 = ks + c * U;
-    const int64_t kw_off = static_cast<int64_t>(min(s0 + ld_step, p.nks - 1)) * 64 +
-                           (ld_unit & 3) * 16;
     if constexpr (DIRECT) {
-    (void)kw_off;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int n = min(wrow(g, nt * 16 + lr), nrows - 1);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t ko = static_cast<int64_t>(min(s0 + u, p.nks - 1)) * 64 + lg * 16;
-        R.w[nt * U + u] = sd::load16_stream(p.w + sd::keep_or_zero(real, static_cast<int64_t>(n) * p.ws + ko));
+        const uint32_t ko = static_cast<uint32_t>(min(s0 + u, p.nks - 1)) * 64u + lg * 16u;
+        R.w[nt * U + u] = wload(n, ko, real);
       }
     }
     } else {
+    const uint32_t kw_off = static_cast<uint32_t>(min(s0 + ld_step, p.nks - 1)) * 64u +
+                            (ld_unit & 3) * 16u;
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int n = min(wrow(g, i * RPI + ld_row), nrows - 1);
-      R.w[i] = sd::load16_stream(p.w + sd::keep_or_zero(real, static_cast<int64_t>(n) * p.ws + kw_off));
-    }
+    for (int i = 0; i < NLD; ++i) R.w[i] = wload(min(wrow(g, i * RPI + ld_row), nrows - 1), kw_off, real);
     }
 #pragma unroll
     for (int u = 0; u < (XL ? 0 : U); ++u) {
@@ -328,19 +330,10 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
       u32x4 xv[MT][2];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        if constexpr (XL && MT >= 2) {
+        if constexpr (XL) {
           const char* xr = xsm + xro[mt] + step * 128 + lg * 32;
           xv[mt][0] = sd::load16(xr);
           xv[mt][1] = sd::load16(xr + 16);
-        } else if constexpr (XL) {
-          if (xok[mt]) {
-            const char* xr = xsm + (mt * 16 + lr) * p.xpitch + step * 128 + lg * 32;
-            xv[mt][0] = sd::load16(xr);
-            xv[mt][1] = sd::load16(xr + 16);
-          } else {
-            xv[mt][0] = u32x4{0u, 0u, 0u, 0u};
-            xv[mt][1] = u32x4{0u, 0u, 0u, 0u};
-          }
         } else if constexpr (SL) {
           xv[mt][0] = sd::silu_mul8<T>(R.x[u][mt][0], R.xu[u][mt][0]);
           xv[mt][1] = sd::silu_mul8<T>(R.x[u][mt][1], R.xu[u][mt][1]);
@@ -502,12 +495,19 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
 
   // ring of D register buffers: item i + D - 1 is loaded while item i computes
   Regs ring[D];
-  auto group_of = [&](int i) { return g0 + (i / nchunks) * gstride; };
+  // (row group, chunk) of the next item to load and of the next to compute,
+  // each advanced one item at a time (uniform selects, no division per item)
+  int lgp = g0, lcp = 0, cgp = g0, ccp = 0;
+  auto advance = [&](int& g, int& c) {
+    const bool wrap = c + 1 == nchunks;
+    c = wrap ? 0 : c + 1;
+    g = wrap ? g + gstride : g;
+  };
 #pragma unroll
   for (int d = 0; d < D - 1; ++d) {
     if (XL && nit == 0) break;
-    const int i = min(d, nit - 1);
-    load(ring[d], group_of(i), i % nchunks, d < nit);
+    load(ring[d], lgp, lcp, d < nit);
+    if (d + 1 < nit) advance(lgp, lcp);  // past the end: the last item again (dummy loads)
   }
   if constexpr (XL) {
     // stage rows m0 .. m0 + rows of x (16-byte units) behind the first weight
@@ -563,20 +563,21 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int cur = it + d;
-      const int ahead = min(cur + D - 1, nit - 1);  // past the end: dummy loads
-      load(ring[(d + D - 1) % D], group_of(ahead), ahead % nchunks, cur + D - 1 < nit);
-      const int gi = group_of(cur), ci = cur % nchunks;
-      compute(ring[d], gi, ci);
-      if (ci + 1 == nchunks) epilogue(gi);
+      // item cur + D - 1 (past the end: dummy loads)
+      load(ring[(d + D - 1) % D], lgp, lcp, cur + D - 1 < nit);
+      if (cur + D < nit) advance(lgp, lcp);
+      compute(ring[d], cgp, ccp);
+      if (ccp + 1 == nchunks) epilogue(cgp);
+      advance(cgp, ccp);
     }
   }
 #pragma unroll
   for (int d = 0; d < D - 1; ++d) {
     const int cur = it + d;
     if (cur >= nit) break;  // wave-uniform (workgroup-uniform when KW > 1)
-    const int gi = group_of(cur), ci = cur % nchunks;
-    compute(ring[d], gi, ci);
-    if (ci + 1 == nchunks) epilogue(gi);
+    compute(ring[d], cgp, ccp);
+    if (ccp + 1 == nchunks) epilogue(cgp);
+    advance(cgp, ccp);
   }
 }
 
@@ -1157,6 +1158,12 @@ int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& nor
   }
   if (M > (1ll << 30) || N > (1ll << 30) || K > (1ll << 30)) {
     sd::set_error("w8a16: dimensions too large");
+    return SD_ERR_UNSUPPORTED;
+  }
+  // the tiled kernel addresses weight bytes with 32-bit offsets (24-bit row stride)
+  if (w_stride_n >= (1ll << 24) || N * w_stride_n >= (1ll << 32)) {
+    sd::set_error("w8a16: the weight matrix must span less than 4 GiB with a row stride below "
+                  "2^24 bytes (N=%lld, stride=%lld)", (long long)N, (long long)w_stride_n);
     return SD_ERR_UNSUPPORTED;
   }
   if (!sd::aligned16(x) || !sd::aligned16(w) || x_stride_m % 8 != 0 || w_stride_n % 16 != 0 ||
