@@ -15,7 +15,9 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libspecdec_amd.so")
+# SPECDEC_AMD_LIBRARY: another build of the same library (a sanitizer build
+# for the host-side checks, for instance)
+LIB_PATH = os.environ.get("SPECDEC_AMD_LIBRARY") or os.path.join(_HERE, "libspecdec_amd.so")
 ABI_VERSION = 2
 
 SD_OK, SD_ERR_VALUE, SD_ERR_UNSUPPORTED, SD_ERR_WORKSPACE, SD_ERR_HIP = range(5)

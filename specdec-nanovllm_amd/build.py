@@ -51,16 +51,37 @@ COMMON_FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compile all sources and link ``libspecdec_amd.so``; returns its path."""
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer build (the C-ABI's
+# argument checks on a machine without a GPU): the host pass only, with an empty
+# device image (no kernel can run from this build), the sanitizer runtime
+# preloaded by the process that opens the library.
+SANITIZE_FLAGS = [
+    "-O1", "-g", "-fno-omit-frame-pointer", "--cuda-host-only",
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined",
+]
+
+
+def build(verbose: bool = False, sanitize: bool = False, out: str | None = None) -> str:
+    """Compile all sources and link ``libspecdec_amd.so`` (or ``out``); returns its
+    path. ``sanitize``: the host-only sanitizer build (no kernels; for the
+    argument-validation tests)."""
     cc = hipcc()
     srcs = sources()
-    tmp = tempfile.mkdtemp(prefix="sd_build_", dir=HERE)
+    lib_path = out or LIB_PATH
+    extra = SANITIZE_FLAGS if sanitize else []
+    tmp = tempfile.mkdtemp(prefix="sd_build_", dir=os.path.dirname(lib_path))
     try:
+        if sanitize:
+            empty = os.path.join(tmp, "empty.fatbin")
+            open(empty, "wb").close()
+            extra = extra + ["-Xclang", "-fcuda-include-gpubinary", "-Xclang", empty]
+
         def compile_one(src: str) -> str:
             obj = os.path.join(tmp, os.path.basename(src) + ".o")
             lang = ["-x", "hip"] if src.endswith(".cpp") else []
-            cmd = [cc, *COMMON_FLAGS, *lang, "-c", src, "-o", obj]
+            cmd = [cc, *COMMON_FLAGS, *extra, *lang, "-c", src, "-o", obj]
             if verbose:
                 print(" ".join(cmd), flush=True)
             r = subprocess.run(cmd, capture_output=True, text=True)
@@ -70,17 +91,17 @@ def build(verbose: bool = False) -> str:
 
         with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
             objs = list(ex.map(compile_one, srcs))
-        out_tmp = LIB_PATH + ".tmp"
+        out_tmp = lib_path + ".tmp"
         cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", out_tmp]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-        os.replace(out_tmp, LIB_PATH)
+        os.replace(out_tmp, lib_path)
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
-    return LIB_PATH
+    return lib_path
 
 
 if __name__ == "__main__":

@@ -312,7 +312,11 @@ __global__ __launch_bounds__(64) void sample_merge_kernel(SampleParams p) {
   if (threadIdx.x == 0) p.out[row] = bi == 0x7fffffff ? 0 : bi;  // an all-NaN row gives token 0
 }
 
-int sample_slices(int32_t vocab) { return (vocab + kSampleSlice - 1) / kSampleSlice; }
+constexpr int kSampleMaxRows = 65535;  // grid y
+
+int sample_slices(int32_t vocab) {
+  return static_cast<int>((static_cast<int64_t>(vocab) + kSampleSlice - 1) / kSampleSlice);
+}
 
 bool is16(int32_t dtype) { return dtype == SD_BF16 || dtype == SD_F16; }
 
@@ -359,8 +363,9 @@ extern "C" int sd_rmsnorm(const void* x, int64_t x_stride, const void* residual,
 namespace {
 
 int run_qk_norm_rope(RopeParams p, int32_t head_dim, int32_t dtype, void* stream) {
-  if (head_dim != 128 || !is16(dtype) || p.tokens < 0 || p.Hq < 0 || p.Hkv < 0 ||
-      p.max_pos <= 0 || p.cs_stride < 128) {
+  if (head_dim != 128 || !is16(dtype) || p.tokens < 0 || p.tokens > (1ll << 40) || p.Hq < 0 ||
+      p.Hkv < 0 || p.Hq > (1 << 20) || p.Hkv > (1 << 20) || p.max_pos <= 0 ||
+      p.max_pos > (1ll << 40) || p.cs_stride < 128 || p.cs_stride > (1ll << 40)) {
     sd::set_error("qk_norm_rope: head_dim 128 and bf16/fp16 only, cos_sin rows of >= 128 "
                   "floats (head_dim=%d dtype=%d stride=%lld)", head_dim, dtype,
                   (long long)p.cs_stride);
@@ -433,6 +438,11 @@ extern "C" int sd_qk_norm_rope_store(void* q, int64_t q_stride_tok, int64_t q_st
     sd::set_error("qk_norm_rope_store: v, caches, slot_mapping and a positive pool needed");
     return SD_ERR_VALUE;
   }
+  if (block_size > (1 << 20) || num_blocks > (1ll << 32)) {
+    sd::set_error("qk_norm_rope_store: pool too large (%lld blocks of %d)", (long long)num_blocks,
+                  block_size);
+    return SD_ERR_UNSUPPORTED;
+  }
   RopeParams p{};
   p.q = static_cast<uint16_t*>(q);
   p.q_stok = q_stride_tok;
@@ -498,6 +508,7 @@ extern "C" int sd_silu_mul(const void* x, int64_t x_stride, void* out, int64_t o
 
 extern "C" size_t sd_sample_workspace_size(int64_t rows, int32_t vocab) {
   if (rows <= 0 || vocab <= 0) return 0;
+  if (rows > kSampleMaxRows) return SIZE_MAX;  // refused by sd_sample
   return static_cast<size_t>(rows) * sample_slices(vocab) * sizeof(float2);
 }
 
@@ -506,9 +517,10 @@ extern "C" int sd_sample(const void* logits, int64_t logits_stride, int32_t dtyp
                          int64_t* out_tokens, void* workspace, size_t workspace_bytes,
                          void* stream) {
   sd::clear_error();
-  if (rows < 0 || vocab <= 0 || (dtype != SD_BF16 && dtype != SD_F16 && dtype != SD_F32)) {
-    sd::set_error("sample: vocab must be positive, logits bf16/fp16/fp32 (vocab=%d dtype=%d)",
-                  vocab, dtype);
+  if (rows < 0 || rows > kSampleMaxRows || vocab <= 0 ||
+      (dtype != SD_BF16 && dtype != SD_F16 && dtype != SD_F32)) {
+    sd::set_error("sample: up to %d rows, vocab positive, logits bf16/fp16/fp32 (rows=%lld "
+                  "vocab=%d dtype=%d)", kSampleMaxRows, (long long)rows, vocab, dtype);
     return SD_ERR_UNSUPPORTED;
   }
   if (rows == 0) return SD_OK;

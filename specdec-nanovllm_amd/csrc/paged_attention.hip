@@ -1209,6 +1209,11 @@ int run_attention(RunMode mode, const NewRows& nr, const void* q, int64_t q_stri
                   "aligned");
     return SD_ERR_UNSUPPORTED;
   }
+  if (!sd::strides_ok({q_stride_tok, q_stride_head, cache_stride_block, cache_stride_pos,
+                       cache_stride_head, bt_stride, out_stride_tok, out_stride_head})) {
+    sd::set_error("paged_attention: strides must lie in [-2^40, 2^40] elements");
+    return SD_ERR_VALUE;
+  }
   if (cache_stride_block < 0 || cache_stride_pos < 0 || cache_stride_head < 0 ||
       cache_stride_pos > (1ll << 25)) {
     sd::set_error("paged_attention: cache strides must be non-negative and the key-row stride "
@@ -1234,7 +1239,8 @@ int run_attention(RunMode mode, const NewRows& nr, const void* q, int64_t q_stri
     if (rc != SD_OK) return rc;
     workspace_bytes = kScratchBytes;
   }
-  if (!workspace || workspace_bytes < need || !sd::aligned16(workspace)) {
+  if (!workspace || workspace_bytes < need || !sd::aligned16(workspace) ||
+      reinterpret_cast<uintptr_t>(workspace) > UINTPTR_MAX - workspace_bytes) {
     sd::set_error("paged_attention: workspace of %zu bytes (16-byte aligned) required, got %zu",
                   need, workspace ? workspace_bytes : (size_t)0);
     return SD_ERR_WORKSPACE;

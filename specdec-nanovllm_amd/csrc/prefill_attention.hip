@@ -339,6 +339,17 @@ extern "C" int sd_prefill_attention(
     sd::set_error("prefill_attention: paged K/V needs block_size, num_blocks, table width");
     return SD_ERR_VALUE;
   }
+  const int64_t max_ctx = static_cast<int64_t>(max_blocks_per_seq) * block_size;
+  if ((block_table && max_ctx > (1ll << 30)) || max_seqlen_q > (1 << 30)) {
+    sd::set_error("prefill_attention: context bound %lld or query length %d too large",
+                  (long long)max_ctx, max_seqlen_q);
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (!sd::strides_ok({q_stride_tok, q_stride_head, kv_stride_tok, kv_stride_head,
+                       kv_stride_block, bt_stride, out_stride_tok, out_stride_head})) {
+    sd::set_error("prefill_attention: strides must lie in [-2^40, 2^40] elements");
+    return SD_ERR_VALUE;
+  }
   if (!sd::aligned16(q) || !sd::aligned16(k) || !sd::aligned16(v) || q_stride_tok % 8 ||
       q_stride_head % 8 || kv_stride_tok % 8 || kv_stride_head % 8 || kv_stride_block % 8 ||
       (reinterpret_cast<uintptr_t>(out) & 7u) || out_stride_tok % 4 || out_stride_head % 4 ||
@@ -360,7 +371,7 @@ extern "C" int sd_prefill_attention(
   p.num_blocks = static_cast<int32_t>(num_blocks > 0x7fffffff ? 0x7fffffff : num_blocks);
   p.bt = block_table;
   p.bt_stride = bt_stride;
-  p.max_ctx = block_table ? max_blocks_per_seq * block_size : 0x7fffffff;
+  p.max_ctx = block_table ? static_cast<int32_t>(max_ctx) : 0x7fffffff;
   p.cu_q = cu_seqlens_q;
   p.cu_k = cu_seqlens_k;
   p.num_seqs = num_seqs;

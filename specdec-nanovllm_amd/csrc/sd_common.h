@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include "specdec_amd.h"
 
 namespace sd {
@@ -365,5 +367,14 @@ inline Span span16(const void* p, int64_t rows, int64_t stride, int64_t width) {
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Strides (in elements) the entry points accept: |stride| <= 2^40 keeps every
+// offset and product they form from the sizes they accept inside int64.
+constexpr int64_t kMaxStride = int64_t(1) << 40;
+inline bool strides_ok(std::initializer_list<int64_t> strides) {
+  for (const int64_t st : strides)
+    if (st < -kMaxStride || st > kMaxStride) return false;
+  return true;
+}
 
 }  // namespace sd

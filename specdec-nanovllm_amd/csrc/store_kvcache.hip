@@ -69,6 +69,18 @@ extern "C" int sd_store_kvcache(const void* key, int64_t key_stride_tok, int64_t
                   (long long)num_blocks);
     return SD_ERR_VALUE;
   }
+  if (num_tokens > (1ll << 31) || num_kv_heads > (1 << 16) || head_dim > (1 << 12) ||
+      block_size > (1 << 20) || num_blocks > (1ll << 32)) {
+    sd::set_error("store_kvcache: sizes too large (tokens=%lld heads=%d head_dim=%d bs=%d "
+                  "blocks=%lld)", (long long)num_tokens, num_kv_heads, head_dim, block_size,
+                  (long long)num_blocks);
+    return SD_ERR_UNSUPPORTED;
+  }
+  if (!sd::strides_ok({key_stride_tok, key_stride_head, value_stride_tok, value_stride_head,
+                       cache_stride_block, cache_stride_pos, cache_stride_head})) {
+    sd::set_error("store_kvcache: strides must lie in [-2^40, 2^40] elements");
+    return SD_ERR_VALUE;
+  }
   if (num_tokens == 0) return SD_OK;
   if (!key || !value || !k_cache || !v_cache || !slot_mapping) {
     sd::set_error("store_kvcache: null pointer argument");

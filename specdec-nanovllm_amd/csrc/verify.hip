@@ -437,14 +437,14 @@ __global__ __launch_bounds__(64) void finish_kernel(VerifyParams p) {
 // kMaxParts (row, slice) partials per sequence.
 int nsplit_for(int32_t V, int32_t k) {
   const int cap = kMaxParts / (2 * k + 1);
-  const int n = (V + 8191) / 8192;
+  const int n = static_cast<int>((static_cast<int64_t>(V) + 8191) / 8192);
   return n < 1 ? 1 : (n > cap ? cap : n);
 }
 
 // Slices of the residual race: ~2048 logits per workgroup (8 per thread), so
 // the per-element work (Philox, log, exp, divides) spreads over many waves.
 int nsplit2_for(int32_t V) {
-  const int n = (V + 2047) / 2048;
+  const int n = static_cast<int>((static_cast<int64_t>(V) + 2047) / 2048);
   return n < 1 ? 1 : (n > 1024 ? 1024 : n);
 }
 
@@ -480,6 +480,7 @@ void launch_pair(int32_t ddt, int32_t tdt, const VerifyParams& p, dim3 g1, dim3 
 
 extern "C" size_t sd_verify_batch_workspace_size(int64_t batch, int32_t k, int32_t vocab) {
   if (batch <= 0 || k <= 0 || vocab <= 0) return 0;
+  if (k > kMaxK || batch > 0x7fffffff) return SIZE_MAX;  // refused by sd_verify_batch
   const int ns = nsplit_for(vocab, k);
   return stats_bytes(batch, k, ns) + parts_bytes(batch, nsplit2_for(vocab)) +
          (static_cast<size_t>(batch) * 2 * k * sizeof(float) + 255) / 256 * 256;
@@ -495,10 +496,10 @@ extern "C" int sd_verify_batch(const void* draft, int64_t draft_stride_b, int64_
                                void* workspace, size_t workspace_bytes, void* stream) {
   sd::clear_error();
   auto ok_dtype = [](int32_t d) { return d == SD_BF16 || d == SD_F16 || d == SD_F32; };
-  if (batch < 0 || k <= 0 || k > kMaxK || vocab <= 0 || !ok_dtype(draft_dtype) ||
-      !ok_dtype(target_dtype)) {
-    sd::set_error("verify_batch: need 1 <= k <= %d, vocab > 0, logits bf16/fp16/fp32 "
-                  "(k=%d vocab=%d)", kMaxK, k, vocab);
+  if (batch < 0 || batch > 0x7fffffff || k <= 0 || k > kMaxK || vocab <= 0 ||
+      !ok_dtype(draft_dtype) || !ok_dtype(target_dtype)) {
+    sd::set_error("verify_batch: need batch < 2^31, 1 <= k <= %d, vocab > 0, logits "
+                  "bf16/fp16/fp32 (batch=%lld k=%d vocab=%d)", kMaxK, (long long)batch, k, vocab);
     return SD_ERR_UNSUPPORTED;
   }
   if (batch == 0) return SD_OK;

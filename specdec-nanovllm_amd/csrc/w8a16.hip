@@ -1160,6 +1160,13 @@ int run_w8a16(const void* x, int64_t x_stride_m, int64_t up, const NormArgs& nor
     sd::set_error("w8a16: dimensions too large");
     return SD_ERR_UNSUPPORTED;
   }
+  if (x_stride_m < 0 || y_stride_m < 0 || w_stride_n < 0 || norm.residual_stride < 0 ||
+      norm.residual_out_stride < 0 ||
+      !sd::strides_ok({x_stride_m, y_stride_m, w_stride_n, norm.residual_stride,
+                       norm.residual_out_stride})) {
+    sd::set_error("w8a16: strides must lie in [0, 2^40] elements");
+    return SD_ERR_VALUE;
+  }
   // the tiled kernel addresses weight bytes with 32-bit offsets (24-bit row stride)
   if (w_stride_n >= (1ll << 24) || N * w_stride_n >= (1ll << 32)) {
     sd::set_error("w8a16: the weight matrix must span less than 4 GiB with a row stride below "
@@ -1285,7 +1292,7 @@ extern "C" int sd_w8a16_silu_linear(const void* gate_up, int64_t gate_up_stride_
                                     void* y, int64_t y_stride_m, int64_t M, int64_t N, int64_t K,
                                     int32_t dtype, void* stream) {
   sd::clear_error();
-  if (gate_up_stride_m < 2 * K) {
+  if (K > 0 && K <= (1ll << 30) && gate_up_stride_m < 2 * K) {  // other K: refused below
     sd::set_error("w8a16_silu: gate_up rows hold 2 K = %lld elements, stride %lld",
                   (long long)(2 * K), (long long)gate_up_stride_m);
     return SD_ERR_VALUE;

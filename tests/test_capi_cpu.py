@@ -153,3 +153,87 @@ def test_w8a16_rejects_overlapping_outputs():
                                _lib.SD_BF16, None, 0, None) == _lib.SD_ERR_VALUE
     assert lib.sd_w8a16_silu_linear(x, 2 * K, w, K, s, _lib.SD_BF16, 0, None, x + 3 * row, N,
                                     M, N, K, _lib.SD_BF16, None) == _lib.SD_ERR_VALUE
+
+
+# ------------------------------------------------------------------ argument sweep
+HOSTILE = {
+    ctypes.c_void_p: [None, 0x1001, 0xFFFFFFFFFFFFF000],
+    ctypes.c_int64: [0, -1, 2**31, 2**62, -(2**63)],
+    ctypes.c_int32: [0, -1, 2**31 - 1, -(2**31)],
+    ctypes.c_float: [float("nan"), float("inf"), -1.0, 0.0],
+    ctypes.c_size_t: [0, 2**63],
+}
+
+
+# Plausible values per entry (argument index -> value), so that the sweep's
+# single-argument mutations reach the checks behind the first ones: decode
+# attention at Qwen3-4B geometry (16 sequences, 32 / 8 heads of 128, 256-token
+# pages), a 128-dim store, head_dim 128 for the RoPE and prefill entries.
+_ATTN = {1: 4096, 2: 128, 5: 256 * 1024, 6: 1024, 7: 128, 8: 64, 9: 256, 11: 16, 12: 16,
+         14: None, 15: None, 16: 1, 17: 16, 18: 16, 19: 32, 20: 8, 21: 128, 23: 0,
+         25: 4096, 26: 128, 28: 1 << 30, 29: 0}
+PLAUSIBLE = {
+    "sd_paged_attention": _ATTN,
+    "sd_paged_attention_partial": _ATTN,
+    "sd_paged_attention_combine": _ATTN,
+    "sd_paged_attention_floor": _ATTN,
+    "sd_paged_attention_noalloc": {i: v for i, v in _ATTN.items() if i < 27} | {27: 0},
+    "sd_paged_attention_store": {1: 1024, 2: 128, 4: 1024, 5: 128}
+                                | {i + 7: v for i, v in _ATTN.items()},
+    "sd_store_kvcache": {1: 1024, 2: 128, 4: 1024, 5: 128, 8: 256 * 1024, 9: 1024, 10: 128,
+                         12: 16, 13: 8, 14: 128, 15: 256, 16: 64, 17: 2},
+    "sd_qk_norm_rope": {1: 4096, 2: 128, 4: 1024, 5: 128, 7: 32, 8: 8, 9: 128, 14: 128,
+                        15: 4096, 16: 0},
+    "sd_prefill_attention": {1: 4096, 2: 128, 5: 1024, 6: 128, 7: 256 * 1024, 8: 64, 9: 256,
+                             11: 16, 12: 16, 15: 64, 16: 1024, 17: 16, 18: 32, 19: 8,
+                             20: 128, 22: 0, 24: 4096, 25: 128},
+}
+
+
+def _baseline(name, argtypes):
+    out = []
+    for i, t in enumerate(argtypes):
+        if t is ctypes.c_void_p:
+            out.append(0x10000000 + i * 0x1000000)  # 16-byte aligned, never dereferenced
+        elif t is ctypes.c_int64:
+            out.append(64)
+        elif t is ctypes.c_int32:
+            out.append(16)
+        elif t is ctypes.c_float:
+            out.append(0.125)
+        else:
+            out.append(0)
+    for i, v in PLAUSIBLE.get(name, {}).items():
+        out[i] = v
+    if argtypes[-1] is ctypes.c_void_p:
+        out[-1] = None  # the stream: a host handle, always the default stream here
+    return out
+
+
+@pytest.mark.skipif(torch.cuda.device_count() > 0,
+                    reason="fake device addresses: only where no GPU can be reached")
+def test_argument_sweep_returns_status_codes():
+    """Every entry point, every argument set in turn to a hostile value (NULL,
+    misaligned or top-of-space pointers, 0 / -1 / extreme sizes, NaN and inf):
+    each call returns a status code and leaves a message, never crashes. Run
+    under AddressSanitizer + UndefinedBehaviorSanitizer by
+    test_capi_sanitized_cpu.py, where an overflow or out-of-bounds access in
+    the host-side checks aborts the run."""
+    lib = _lib.load()
+    calls = 0
+    for name, (res, argtypes) in _lib.SIGNATURES.items():
+        if not argtypes:
+            continue
+        fn = getattr(lib, name)
+        base = _baseline(name, argtypes)
+        mutable = argtypes[:-1] if argtypes[-1] is ctypes.c_void_p else argtypes
+        for i, t in enumerate(mutable):
+            for v in HOSTILE[t]:
+                args = list(base)
+                args[i] = v
+                rc = fn(*args)
+                calls += 1
+                if res is ctypes.c_int:
+                    assert 0 <= rc <= _lib.SD_ERR_HIP, (name, i, v, rc)
+                    assert isinstance(lib.sd_last_error(), bytes)
+    assert calls > 500
