@@ -14,6 +14,13 @@
  *
  * Dtype codes: SD_BF16, SD_F16 for activations/caches; scales may also be
  * SD_F32. Strides are in ELEMENTS of the tensor they describe.
+ *
+ * Bounds: every stride must lie within +-2^40 elements (W8A16 strides are
+ * non-negative), and sizes past what one GPU could hold are refused before any
+ * arithmetic on them (sequence and row counts below 2^31, page pools below
+ * 2^32 blocks, context bounds below 2^30 keys). A refused call returns
+ * SD_ERR_VALUE or SD_ERR_UNSUPPORTED and launches nothing; a workspace query
+ * for such sizes returns SIZE_MAX.
  */
 #ifndef SPECDEC_AMD_H
 #define SPECDEC_AMD_H
