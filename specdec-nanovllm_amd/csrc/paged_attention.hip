@@ -837,8 +837,8 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   const int n = steps_of(p, si.L);
 
   // STORE: the new rows' key / value / slot and this row's q, loaded now
-  f32x4 qv = {0.f, 0.f, 0.f, 0.f}, kn[kNewMax], vn[kNewMax];
-  int64_t sn[kNewMax];
+  f32x4 qv = {0.f, 0.f, 0.f, 0.f}, kn[kNewMax] = {}, vn[kNewMax] = {};
+  int64_t sn[kNewMax] = {};
   if constexpr (STORE) {
     if (live && sl == 0) {
       qv = load4f<T>(p.q + qt * p.q_stok + static_cast<int64_t>(h * p.G + g) * p.q_shead + d4);
@@ -947,11 +947,41 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
       o = o * r + w * vv;
       M = mn;
     };
+    if (si.nq == 1) {  // decode: one new key (uniform over the row's lanes)
+      if (L - 1 >= 0) merge_new(0, kn[0], vn[0], sn[0]);
+    } else {
+      // several new keys: their unstored cache rows and their dot products first,
+      // the butterflies of all keys interleaved (each a chain of five dependent
+      // exchanges), then the merges in key order (the same operations in the
+      // same order as one key at a time)
+      bool use[kNewMax];
+      float dot[kNewMax];
 #pragma unroll
-    for (int j = 0; j < kNewMax; ++j) {  // uniform over the row's lanes
-      if (j >= si.nq) break;
-      if (L - si.nq + j < 0 || j > qi) continue;
-      merge_new(j, kn[j], vn[j], sn[j]);
+      for (int j = 0; j < kNewMax; ++j) {  // uniform over the row's lanes
+        use[j] = j < si.nq && j <= qi && L - si.nq + j >= 0;
+        if (use[j] && !(sn[j] >= 0 && sn[j] < p.num_slots)) {  // not stored: the cache row stays
+          const int64_t crow = kv_row(p, btrow, L - si.nq + j) + static_cast<int64_t>(h) * p.c_shead;
+          kn[j] = load4f<T>(p.kc + crow + d4);
+          vn[j] = load4f<T>(p.vc + crow + d4);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kNewMax; ++j)
+        dot[j] = use[j] ? qv.x * kn[j].x + qv.y * kn[j].y + qv.z * kn[j].z + qv.w * kn[j].w : 0.f;
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1)
+#pragma unroll
+        for (int j = 0; j < kNewMax; ++j) dot[j] += __shfl_xor(dot[j], off);
+#pragma unroll
+      for (int j = 0; j < kNewMax; ++j) {
+        if (!use[j]) continue;
+        const float sj = dot[j] * p.scale_log2;
+        const float mn = fmaxf(M, sj);
+        const float r = exp2f(M - mn), w = exp2f(sj - mn);
+        l = l * r + w;
+        o = o * r + w * vn[j];
+        M = mn;
+      }
     }
     for (int j = kNewMax; j < si.nq; ++j) {
       if (L - si.nq + j < 0 || j > qi) continue;
