@@ -890,7 +890,7 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
           const int64_t e = base + static_cast<int64_t>(c0 + u) * run_stride;
           if (c0 + u < u1) {
             part[u] = ml[e];
-            a[u] = __builtin_bit_cast(f32x4, sd::load16(p.ws_acc + e * kD + d4));
+            a[u] = __builtin_bit_cast(f32x4, sd::load16_stream(p.ws_acc + e * kD + d4));
           } else {
             part[u] = make_float2(-INFINITY, 0.f);
             a[u] = f32x4{0.f, 0.f, 0.f, 0.f};
