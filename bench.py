@@ -22,6 +22,8 @@ Also reported on the same JSON line:
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --profile-pass   (few launches of each kernel + a copy of
                                          known size, for rocprofv3 counter runs)
+       python bench.py --twin-pass      (the attention main kernel and its read-only
+                                         floor twin, C2 B=32 then C3, for counter runs)
 """
 from __future__ import annotations
 
@@ -51,6 +53,8 @@ def parse():
     ap.add_argument("--no-draft-chain", action="store_true",
                     help="skip the C5 draft-chain extra (its thousands of launches swamp a trace)")
     ap.add_argument("--profile-pass", action="store_true")
+    ap.add_argument("--twin-pass", action="store_true",
+                    help="main kernel and floor twin, 3 launches each, C2 B=32 then C3")
     ap.add_argument("--draft-chain-only", type=int, default=0, metavar="B",
                     help="only the fused C5 draft chain at batch B, replayed a few times "
                          "(for a kernel trace); prints us per draft step")
@@ -463,6 +467,36 @@ def bench_draft_chain(workloads_mod, torch, reps=5):
 
 
 # ---------------------------------------------------------------------------- profile
+def twin_pass(ops, workloads, torch):
+    """The attention main kernel (`twin="main"`) and its read-only floor twin, three
+    launches each: C2 decode B=32, then C3 verify (plain attention), so counter runs
+    can set the main kernel's instructions and waits against its access pattern's."""
+    dev = "cuda"
+    c = workloads.decode_case(32, seed=0, sets=1)
+    bt, lens = c["tables"][0].to(dev), c["lens"].to(dev)
+    out = torch.empty_like(c["q"])
+    ws = torch.empty(ops.paged_attention_workspace_bytes(32, 1, 32, 8, bt.shape[1] * 256,
+                                                         device=dev),
+                     dtype=torch.uint8, device=dev)
+    for twin in ("main", "floor"):
+        for _ in range(3):
+            ops.paged_attention(c["q"], c["k_cache"], c["v_cache"], bt, c["scale"],
+                                context_lens=lens, out=out, twin=twin, workspace=ws)
+    v = workloads.verify_case(seed=0, sets=1)
+    vt, cuq, cuk = v["tables"][0].to(dev), v["cu_q"].to(dev), v["cu_k"].to(dev)
+    vo = torch.empty_like(v["q"])
+    vws = torch.empty(ops.paged_attention_workspace_bytes(8, v["k"] + 1, 32, 8,
+                                                          vt.shape[1] * 256, device=dev),
+                      dtype=torch.uint8, device=dev)
+    for twin in ("main", "floor"):
+        for _ in range(3):
+            ops.paged_attention(v["q"], v["k_cache"], v["v_cache"], vt, v["scale"],
+                                cu_seqlens_k=cuk, cu_seqlens_q=cuq, max_seqlen_q=v["k"] + 1,
+                                out=vo, twin=twin, workspace=vws)
+    torch.cuda.synchronize()
+    print(json.dumps({"twin_pass": True}))
+
+
 def profile_pass(ops, workloads, torch):
     """A few launches of each kernel plus a 512 MiB device copy (known bytes) so
     rocprofv3 counter runs can be scaled; prints what ran."""
@@ -531,6 +565,9 @@ def main():
         sys.exit(1)
     if args.profile_pass:
         profile_pass(ops, workloads, torch)
+        return
+    if args.twin_pass:
+        twin_pass(ops, workloads, torch)
         return
     if args.draft_chain_only:
         from specdec_nanovllm_amd.draft_chain import DraftChain
