@@ -520,6 +520,7 @@ void paged_attn_main(AttnParams p) {
   uint16_t* kl = reinterpret_cast<uint16_t*>(tiles);
   uint16_t* vl = kl + kStep * kKPitch;
   u32x4 fold = {0u, 0u, 0u, 0u};  // FLOOR: every loaded word is consumed here
+  const sd::XorAddr xa = sd::xor_addr();  // lanes of the row-maximum exchanges
 
   auto compute_step = [&](StepRegs& R, int cj, int par) {
     const int tb = cj * p.col_keys + ks * kStep;
@@ -574,24 +575,35 @@ void paged_attn_main(AttnParams p) {
     //      and key 16 + 4 lg + (j - 4) (j >= 4), the order S^T already holds.
     u32x4 pop[RT], plo[RT];
     // every row sees every key of this slice: no causal / length mask needed
+    // (a wave-uniform branch, so full steps skip the mask's selects)
     const bool full = tb + kStep - 1 <= min(si.causal, si.L - 1);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[rt][tt][i] *= p.scale_log2;
+    }
+    if (!full) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int tok = tb + tt * 16 + lg * 4 + i;
+            // lim < L: also masks keys past the end
+            sc[rt][tt][i] = tok <= lim[rt] ? sc[rt][tt][i] : -INFINITY;
+          }
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       float mloc = -INFINITY;
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float s = sc[rt][tt][i] * p.scale_log2;
-          if (!full) {
-            const int tok = tb + tt * 16 + lg * 4 + i;
-            s = (tok <= lim[rt]) ? s : -INFINITY;  // lim < L: also masks keys past the end
-          }
-          sc[rt][tt][i] = s;
-          mloc = fmaxf(mloc, s);
-        }
-      }
-      mloc = sd::max_over_groups(mloc);
+        for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, sc[rt][tt][i]);
+      mloc = sd::max_over_groups(mloc, xa);
       const float mnew = fmaxf(m_run[rt], mloc);
       const float mb = (mnew == -INFINITY) ? 0.f : mnew;
       float pv[8];

@@ -49,8 +49,10 @@ template <> struct Elem<_Float16> {
 // rounding where the source says two): without it the bits of an fp16 output
 // near a rounding midpoint depend on which form the compiler picked for that
 // output, so two kernels computing the same fp32 value could disagree.
+// bf16 has no such fused form on gfx950 (v_cvt_pk_bf16_f32 takes the fp32
+// value), so only the fp16 conversion carries the fence.
 template <typename T> __device__ __forceinline__ T round16(float x) {
-  asm("" : "+v"(x));
+  if constexpr (sizeof(T) == 2 && !__is_same(T, __bf16)) asm("" : "+v"(x));
   return static_cast<T>(x);
 }
 // fp32 -> 16-bit storage bits, round to nearest even.
@@ -130,6 +132,20 @@ __device__ __forceinline__ void wave_lds_sync() {
 __device__ __forceinline__ float max_over_groups(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
   v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+// The same with the byte addresses of lanes l ^ 16 and l ^ 32 formed once by
+// the caller (ds_bpermute operands), for loops that exchange every step.
+struct XorAddr {
+  int a16, a32;
+};
+__device__ __forceinline__ XorAddr xor_addr() {
+  const int l = threadIdx.x & 63;
+  return XorAddr{(l ^ 16) << 2, (l ^ 32) << 2};
+}
+__device__ __forceinline__ float max_over_groups(float v, const XorAddr& x) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_bpermute(x.a16, __float_as_int(v))));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_bpermute(x.a32, __float_as_int(v))));
   return v;
 }
 __device__ __forceinline__ float sum_over_groups(float v) {
