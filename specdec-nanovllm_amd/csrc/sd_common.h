@@ -59,9 +59,15 @@ template <typename T> __device__ __forceinline__ T round16(float x) {
 template <typename T> __device__ __forceinline__ uint16_t to_bits(float x) {
   return __builtin_bit_cast(uint16_t, round16<T>(x));
 }
-// Pack two fp32 into one dword of two 16-bit values (lo in bits 0..15).
+// Pack two fp32 into one dword of two 16-bit values (lo in bits 0..15), each
+// rounded to nearest even (bf16: one v_cvt_pk_bf16_f32 for the pair).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return static_cast<uint32_t>(to_bits<T>(lo)) | (static_cast<uint32_t>(to_bits<T>(hi)) << 16);
+  if constexpr (__is_same(T, __bf16))
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+  else
+    return static_cast<uint32_t>(to_bits<T>(lo)) | (static_cast<uint32_t>(to_bits<T>(hi)) << 16);
 }
 template <typename T> __device__ __forceinline__ float from_bits(uint16_t b) {
   return static_cast<float>(__builtin_bit_cast(T, b));
@@ -70,10 +76,17 @@ template <typename T> __device__ __forceinline__ float from_bits(uint16_t b) {
 // a = float(hi_a) + float(lo_a) to ~2^-17 relative (hi and lo each RNE).
 template <typename T>
 __device__ __forceinline__ void split_pack(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const T ha = round16<T>(a), hb = round16<T>(b);
-  hi = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
-       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
-  lo = pack2<T>(a - static_cast<float>(ha), b - static_cast<float>(hb));
+  if constexpr (__is_same(T, __bf16)) {
+    // a bf16 is the top half of its fp32: the rounded values are the packed
+    // word's halves moved into place
+    hi = pack2<T>(a, b);
+    lo = pack2<T>(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+  } else {
+    const T ha = round16<T>(a), hb = round16<T>(b);
+    hi = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
+    lo = pack2<T>(a - static_cast<float>(ha), b - static_cast<float>(hb));
+  }
 }
 
 __device__ __forceinline__ u32x4 load16(const void* p) {
