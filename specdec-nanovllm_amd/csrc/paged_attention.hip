@@ -603,9 +603,23 @@ void paged_attn_main(AttnParams p) {
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, sc[rt][tt][i]);
-      mloc = sd::max_over_groups(mloc, xa);
-      const float mnew = fmaxf(m_run[rt], mloc);
-      const float mb = (mnew == -INFINITY) ? 0.f : mnew;
+      // lazy row maximum: exchanged across the row's lanes, and the running
+      // sums rescaled, only when some score of the wave exceeds its row's
+      // running maximum by more than 8 (log2 units). Otherwise the old maximum
+      // stays the reference, so P <= 2^8: well inside the range of the fp32
+      // sums and of the hi + lo split below, and acc / l does not depend on the
+      // reference chosen (the partials carry it as their m).
+      // The vote is wave-wide, so every lane of a row keeps the same maximum.
+      if (__any(mloc > m_run[rt] + 8.f)) {
+        mloc = sd::max_over_groups(mloc, xa);
+        const float mnew = fmaxf(m_run[rt], mloc);
+        const float alpha = sd::fast_exp2(m_run[rt] - ((mnew == -INFINITY) ? 0.f : mnew));
+        l_run[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[rt][dt] *= alpha;
+        m_run[rt] = mnew;
+      }
+      const float mb = (m_run[rt] == -INFINITY) ? 0.f : m_run[rt];
       float pv[8];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -615,16 +629,7 @@ void paged_attn_main(AttnParams p) {
       float ps = 0.f;
 #pragma unroll
       for (int q = 0; q < 8; ++q) ps += pv[q];
-      // rescale the running sums only when some row's maximum grew (rare after
-      // the first keys); alpha = 1 for the others
-      if (__any(mnew > m_run[rt])) {
-        const float alpha = sd::fast_exp2(m_run[rt] - mb);
-        l_run[rt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[rt][dt] *= alpha;
-      }
       l_run[rt] += ps;
-      m_run[rt] = mnew;
       // P = hi + lo in two 16-bit operands: P.V keeps ~16 mantissa bits of P
       // instead of the 8 (bf16) a single rounding would leave.
       uint32_t hi[4], lo[4];

@@ -1,11 +1,12 @@
 """GPU parity of paged decode / verify attention against the numpy oracle.
 
-Tolerance: |o - ref| <= 2e-3 + 1e-2 |ref| elementwise,
+Tolerance (the stated bound for this path): |o - ref| <= 2e-3 + 1e-2 |ref| elementwise,
 ref = float64 attention of the same bf16/fp16 inputs. Covers the C1/C2/C3
 configurations, edge lengths around the 32/64/256-token tiles and pages,
 padding rows, split counts, page sizes, head-major pages, GQA ratios, fp16,
-ragged verify rows, placement/width invariance, determinism and HIP-graph
-replay, plus the reference-mirror entry points and their error behaviour.
+ragged verify rows, scores whose row maximum rises, spikes or falls along the
+keys (the running maximum re-based inside a walk), placement/width invariance,
+determinism and HIP-graph replay, plus the reference-mirror entry points and their error behaviour.
 """
 import math
 
@@ -67,7 +68,7 @@ def run_decode(q, kc, vc, bt, lens, **kw):
                                context_lens=lens.to(DEV), **kw)
 
 
-# ------------------------------------------------------------------ BASELINE configs
+# ----------------------------------------------------- benchmark configurations
 @pytest.mark.parametrize("batch", [1, 8, 32])
 def test_c2_decode_step(batch):
     case = workloads.decode_case(batch, seed=100 + batch)
@@ -194,6 +195,62 @@ def test_verify_ragged_rows(hq, hkv):
                               cu_seqlens_q=cu_q.to(DEV), max_seqlen_q=max(nq))
     ref = oracle(q, kc, vc, bt, lens, 128 ** -0.5, cu_q)
     assert_close_attn(to_np(out), ref, what="ragged verify")
+
+
+def _steer_scores(q, kc, bt, lens, profile, bs=256):
+    """Add c(t) u to key t of every sequence and 10 u to every query (u a unit
+    vector), so each score gains about 10 c(t) / sqrt(D) nats on top of the
+    N(0, 1) noise: "rising" grows the row maximum steadily along the walk
+    (about 50 log2 units end to end, so the running maximum is re-based many
+    times inside one split), "spike" puts one late key about 75 log2 units
+    above the rest, "falling" keeps the maximum in the first keys."""
+    d = q.shape[-1]
+    u = torch.ones(d, device=DEV) / math.sqrt(d)
+    for b, n in enumerate(lens.tolist()):
+        t = torch.arange(n, dtype=torch.float32)
+        if profile == "rising":
+            c = 40.0 * t / max(n - 1, 1)
+        elif profile == "spike":
+            c = torch.where(t == max(n - 5, 0), 60.0, 0.0)
+        else:
+            c = 40.0 * (1.0 - t / max(n - 1, 1))
+        ti = torch.arange(n)
+        pages = bt[b, ti // bs].long().to(DEV)
+        offs = (ti % bs).to(DEV)
+        kc[pages, offs] = (kc[pages, offs].float() + c.to(DEV)[:, None, None] * u).to(kc.dtype)
+    return (q.float() + 10.0 * u).to(q.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("profile", ["rising", "spike", "falling"])
+def test_running_maximum_moves_along_the_walk(profile, dtype):
+    q, kc, vc, bt, lens = random_case([3000, 1500, 77, 300], dtype=dtype, seed=23)
+    q = _steer_scores(q, kc, bt, lens, profile)
+    ref = oracle(q, kc, vc, bt, lens, 128 ** -0.5)
+    for splits in (None, 1, 5):
+        kw = {} if splits is None else {"num_splits": splits}
+        out = run_decode(q, kc, vc, bt, lens, **kw)
+        assert_close_attn(to_np(out), ref, what=f"{profile} splits={splits}")
+
+
+@pytest.mark.parametrize("profile", ["rising", "spike"])
+def test_running_maximum_moves_verify_rows(profile):
+    nq = [6, 1, 4]
+    keys = [2600, 700, 260]
+    lens = torch.tensor(keys, dtype=torch.int32)
+    g = torch.Generator().manual_seed(79)
+    bt = workloads.block_tables_for(keys, 256, 20, g, 12)[0]
+    dg = workloads.device_generator(DEV, 80)
+    kc = torch.randn((20, 256, 8, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    vc = torch.randn((20, 256, 8, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(nq)]), dtype=torch.int32)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(keys)]), dtype=torch.int32)
+    q = torch.randn((int(cu_q[-1]), 32, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    q = _steer_scores(q, kc, bt, lens, profile)
+    out = ops.paged_attention(q, kc, vc, bt.to(DEV), 128 ** -0.5, cu_seqlens_k=cu_k.to(DEV),
+                              cu_seqlens_q=cu_q.to(DEV), max_seqlen_q=max(nq))
+    ref = oracle(q, kc, vc, bt, lens, 128 ** -0.5, cu_q)
+    assert_close_attn(to_np(out), ref, what=f"{profile} verify")
 
 
 def test_placement_and_width_invariance_bitwise():
