@@ -1064,9 +1064,13 @@ struct Plan {
   int64_t slots;  // partial slots: (runs + num_seqs) * Hkv
 };
 
-// num_splits == 0: one resident set of waves (4 SIMDs x main_occupancy per
-// compute unit, one wave per kv head of a run) shares all the columns, at
-// least one column (two for two row tiles) per run.
+// num_splits == 0: one wave per SIMD (4 per compute unit, one wave per kv
+// head of a run, or per half column / row tile) shares all the columns, at
+// least one column per run. Against two waves per SIMD (the occupancy the
+// kernel is built for) the runs are twice as long and leave half the partials;
+// store + attention measured (16 page sets, same process): C2 B = 32 57.1 ->
+// 55.8 us, B = 8 28.3 -> 26.1, B = 4 20.9 -> 19.1, B = 2 17.0 -> 14.8, B = 1
+// level; C3 verify 26.0 -> 25.3, B = 16 verify 40.7 -> 38.1.
 // num_splits > 0: num_splits runs per sequence on average, the meaning of the
 // reference's `splits` (KV splits per sequence).
 Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
@@ -1085,9 +1089,7 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
     runs = static_cast<int64_t>(num_splits) * num_seqs;
     pl.min_steps = 1;
   } else {
-    // waves per SIMD of the instance that runs (a tile-split wave holds one tile)
-    const int occ = pl.RT == 1 || pl.TS == 2 ? main_occupancy<1>() : main_occupancy<2>();
-    runs = static_cast<int64_t>(sd::device_cus()) * 4 * occ / (Hkv * pl.KS * pl.TS);
+    runs = static_cast<int64_t>(sd::device_cus()) * 4 / (Hkv * pl.KS * pl.TS);
     // at least 64 keys per run with two tiles on one wave
     pl.min_steps = pl.RT == 1 || pl.KS == 2 || pl.TS == 2 ? 1 : 2;
   }
