@@ -99,6 +99,70 @@ def time_replays(graphs, steps, warmup, torch, per_launch=False):
     return start.elapsed_time(end) / steps
 
 
+def time_groups(graph, per_replay, torch, groups=5, min_launches=20, warmup=2):
+    """Per-launch time of the launches one replay of ``graph`` holds
+    (``per_replay`` of them): HIP events on the current stream around each of
+    ``groups`` groups of back-to-back replays, each group at least
+    ``min_launches`` launches; returns (median, min, max) in ms over the
+    groups' per-launch means. The decision protocol for the roofline legs and
+    the per-shape rows: a median of groups, not one mean, with the spread."""
+    import statistics
+    reps = max(1, math.ceil(min_launches / per_replay))
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(groups):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) / (reps * per_replay))
+    return statistics.median(ts), min(ts), max(ts)
+
+
+def us3(t):
+    """(median, min, max) ms -> {"us", "min_us", "max_us"}."""
+    return {"us": round(t[0] * 1e3, 2), "min_us": round(t[1] * 1e3, 2),
+            "max_us": round(t[2] * 1e3, 2)}
+
+
+def read_ceiling(ops, torch):
+    """The box's streaming-read ceiling (sd_stream_read over a 1 GiB buffer,
+    4 / 6 / 8 workgroups per CU, the best median kept) and, as the reference
+    measured its own (nanovllm/kernels/README.md:27-35), a plain 512 MiB
+    device copy counted as read + write bytes."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(3)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    best = None
+    sweep = {}
+    for per_cu in (4, 6, 8):
+        g = graph_of(lambda: [ops.stream_read(buf, sink, per_cu * cus) for _ in range(4)], torch)
+        t = time_groups(g, 4, torch, groups=5, min_launches=8)
+        del g
+        gbs = (1 << 30) / (t[0] * 1e-3) / 1e9
+        sweep[f"{per_cu}_per_cu"] = round(gbs, 1)
+        if best is None or gbs > best[0]:
+            best = (gbs, per_cu, t)
+    del buf
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    g = graph_of(lambda: [dst.copy_(src) for _ in range(4)], torch)
+    tc = time_groups(g, 4, torch, groups=5, min_launches=8)
+    del g, src, dst
+    torch.cuda.empty_cache()
+    return {"read_GBps": round(best[0], 1), "read_workgroups_per_cu": best[1],
+            "read_bytes": 1 << 30, "read_us": round(best[2][0] * 1e3, 2),
+            "read_sweep_GBps": sweep,
+            "copy_GBps": round(2 * (512 << 20) / (tc[0] * 1e-3) / 1e9, 1),
+            "copy_bytes_each_way": 512 << 20,
+            "note": "sd_stream_read: grid-stride 16-byte nontemporal loads, median of 5 "
+                    "groups; copy: torch copy_ of 512 MiB, read + write bytes"}
+
+
 def time_steps(chain_graph, step_graphs, steps, warmup, torch):
     """ms per decode step over exactly ``steps`` steps: steps // n replays of
     ``chain_graph`` (the n = len(step_graphs) steps back to back in one graph,
@@ -302,8 +366,9 @@ def bench_verify(ops, workloads, torch, steps):
                                                out=out, **kw)
         fns = [one(i) for i in range(sets)]
         return lambda: [f() for f in fns]
-    reps = max(3, steps // sets)
-    ms = time_replays([graph_of(chain(True), torch)], reps, 2, torch) / sets
+    del steps
+    t = time_groups(graph_of(chain(True), torch), sets, torch)
+    ms = t[0]
     nbytes = (attn_bytes(case["keys"].tolist(), 32, 8, 128, 2, q_rows=case["k"] + 1)
               + case["slots"].numel() * 8 * 128 * 2 * 2 * 2)
     flops = sum(4 * 32 * 128 * (case["k"] + 1) * int(L) for L in case["keys"])
@@ -311,11 +376,13 @@ def bench_verify(ops, workloads, torch, steps):
                      f"{sets} calls per graph", "us": round(ms * 1e3, 2),
            "GBps": round(nbytes / ms / 1e6, 1), "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
            "TFLOPs": round(flops / ms / 1e9, 2), "seed": case["seed_used"],
-           "algorithmic_bytes": nbytes}
+           "algorithmic_bytes": nbytes, "minmax_us": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
+           "timing": "median of 5 groups of >= 20 calls"}
     # the plain (non-storing) call and its twins over the same keys
     for twin, key in ((None, "attention_us"), ("main", "main_us"), ("floor", "floor_us")):
-        t = time_replays([graph_of(chain(False, twin), torch)], reps, 2, torch) / sets
-        res[key] = round(t * 1e3, 2)
+        tt = time_groups(graph_of(chain(False, twin), torch), sets, torch)
+        res[key] = round(tt[0] * 1e3, 2)
+        res[key.replace("_us", "_minmax_us")] = [round(tt[1] * 1e3, 2), round(tt[2] * 1e3, 2)]
     return res
 
 
@@ -347,12 +414,15 @@ def bench_decode_batch(ops, workloads, torch, B, steps):
                                                             "workspace": ws}))
                for i in range(sets)]
         return lambda: [f() for f in fns]
-    reps = max(2, steps // sets)
-    res = {"config": f"C2 decode step B={B} (store + attention), {sets} page sets"}
+    del steps
+    res = {"config": f"C2 decode step B={B} (store + attention), {sets} page sets, median of "
+                     "5 groups of >= 20 calls"}
     for name, kw in (("step_us", {"store": True}), ("attention_us", {}),
                      ("main_us", {"twin": "main"}), ("floor_us", {"twin": "floor"})):
         g = graph_of(chain(**kw), torch)
-        res[name] = round(time_replays([g], reps, 2, torch) / sets * 1e3, 2)
+        t = time_groups(g, sets, torch)
+        res[name] = round(t[0] * 1e3, 2)
+        res[name.replace("_us", "_minmax_us")] = [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)]
         del g
     nbytes = decode_bytes(case["lens"].tolist(), 32, 8, 128, 2, B)
     res["GBps"] = round(nbytes / res["step_us"] / 1e3, 1)
@@ -363,31 +433,105 @@ def bench_decode_batch(ops, workloads, torch, B, steps):
     return res
 
 
+def bench_ctx_sweep(ops, workloads, torch):
+    """B = 1 decode at Qwen3-4B attention geometry over context lengths 256 -
+    4096, the reference's latency curve (nanovllm/kernels/README.md:266-275):
+    the attention op (main + combine) and the decode step (fused store +
+    attention), us per call as the median of 5 groups over chains of 32
+    calls, each call on its own page set."""
+    sets = 32
+    case = workloads.decode_case(1, seed=7, sets=sets, ctx_range=(4096, 4096))
+    tables = [t.cuda() for t in case["tables"]]
+    out = torch.empty_like(case["q"])
+    ws = torch.empty(ops.paged_attention_workspace_bytes(1, 1, 32, 8, 4096, device="cuda"),
+                     dtype=torch.uint8, device="cuda")
+    rows = []
+    for L in (256, 512, 1024, 2048, 4096):
+        lens = torch.full((1,), L, dtype=torch.int32, device="cuda")
+        slots = [(t[0, (L - 1) // 256].long() * 256 + (L - 1) % 256).to(torch.int32).view(1)
+                 for t in tables]
+
+        def chain(store):
+            if store:
+                return lambda: [ops.paged_attention(case["q"], case["k_cache"], case["v_cache"],
+                                                    tables[i], case["scale"], context_lens=lens,
+                                                    out=out, key=case["k_new"],
+                                                    value=case["v_new"], slot_mapping=slots[i])
+                                for i in range(sets)]
+            return lambda: [ops.paged_attention(case["q"], case["k_cache"], case["v_cache"],
+                                                tables[i], case["scale"], context_lens=lens,
+                                                out=out, workspace=ws) for i in range(sets)]
+        row = {"ctx": L}
+        for key, store in (("attention_us", False), ("step_us", True)):
+            g = graph_of(chain(store), torch)
+            t = time_groups(g, sets, torch, groups=5, min_launches=32)
+            del g
+            row[key] = round(t[0] * 1e3, 2)
+            row[key.replace("_us", "_minmax_us")] = [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)]
+        nbytes = attn_bytes([L], 32, 8, 128, 2)
+        row["attention_GBps"] = round(nbytes / row["attention_us"] / 1e3, 1)
+        rows.append(row)
+    del case
+    torch.cuda.empty_cache()
+    return {"config": "B=1, 32q/8kv/128 bf16, 256-token pages, 32 page sets (one per call), "
+                      "median of 5 groups of >= 32 calls", "rows": rows}
+
+
 def bench_w8a16(ops, workloads, torch, steps):
     """Each shape x M: one HIP graph holding a chain of calls over `copies`
     distinct weight copies (> 2 x the 256 MB MALL in total, so every call
-    streams its weight from HBM, as a model forward does); us per call =
-    graph time / calls."""
+    streams its weight from HBM, as a model forward does); us per call = the
+    median over 5 groups of >= 20 calls (min / max beside it). Beside each
+    row: the load-only twin (sd_w8a16_floor, same plan and loads, no math) and,
+    at M in {1, 16}, the dense bf16 linear torch runs for the same shape
+    (F.linear, hipBLASLt) over bf16 weight copies, as the reference compares
+    its int8 path with the bf16 GEMM (docs/W8A16量化-开发记录.md:264-275,
+    scripts/bench_int8_gemm.py:138-146)."""
+    import torch.nn.functional as F
     rows = []
+    del steps
     for name, N, K in workloads.W8A16_SHAPES:
         for M in workloads.W8A16_MS:
             copies = max(2, math.ceil(2 * 256e6 / (N * K)))
             base = workloads.w8a16_case(M, N, K, seed=N + M)
             ws = [base["w"]] + [torch.roll(base["w"], i, 0) for i in range(1, copies)]
             y = torch.empty((M, N), dtype=torch.float16, device="cuda")
-
-            def chain():
-                for w in ws:
-                    ops.w8a16_linear(base["x"], w, base["s"], out=y)
-            g = graph_of(chain, torch)
-            reps = max(3, steps // copies)
-            ms = time_replays([g], reps, 2, torch) / copies
             nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
-            rows.append({"shape": name, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
-                         "GBps": round(nbytes / ms / 1e6, 1),
-                         "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4)})
-            del ws, g
+            row = {"shape": name, "M": M, "N": N, "K": K}
+            for key, twin in (("us", None), ("floor", "floor")):
+                g = graph_of(lambda: [ops.w8a16_linear(base["x"], w, base["s"], out=y, twin=twin)
+                                      for w in ws], torch)
+                t = time_groups(g, copies, torch)
+                del g
+                if twin is None:
+                    row.update(us3(t))
+                    row["GBps"] = round(nbytes / t[0] / 1e6, 1)
+                    row["frac"] = round(nbytes / t[0] / 1e6 / PEAK_HBM_GBS, 4)
+                else:
+                    row["floor_us"] = round(t[0] * 1e3, 2)
+            del ws
             torch.cuda.empty_cache()
+            if M in (1, 16):
+                bcopies = max(2, math.ceil(2 * 256e6 / (2 * N * K)))
+                gen = torch.Generator(device="cuda").manual_seed(N + K)
+                wb = [(torch.randn((N, K), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+                      for _ in range(bcopies)]
+                xb = base["x"].to(torch.bfloat16)
+                try:
+                    g = graph_of(lambda: [F.linear(xb, w) for w in wb], torch)
+                    t = time_groups(g, bcopies, torch)
+                    del g
+                    bbytes = 2 * N * K + 2 * M * K + 2 * M * N
+                    row["bf16_linear_us"] = round(t[0] * 1e3, 2)
+                    row["bf16_linear_GBps"] = round(bbytes / t[0] / 1e6, 1)
+                    row["int8_speedup_vs_bf16"] = round(t[0] * 1e3 / row["us"], 2)
+                except RuntimeError as e:  # capture refused: say so, no number
+                    row["bf16_linear_us"] = None
+                    row["bf16_linear_note"] = str(e)[:120]
+                del wb
+                torch.cuda.empty_cache()
+            rows.append(row)
+            del base
     return rows
 
 
@@ -445,16 +589,19 @@ def bench_draft_chain(workloads_mod, torch, reps=5):
         parts = {}
         for name, fn in (("attention", ch.attention_chain), ("gemv", ch.gemv_chain)):
             g = graph_of(fn, torch)
-            parts[name] = time_replays([g], reps, 1, torch) * 1e3 / ch.k
+            parts[name] = time_groups(g, ch.k, torch, groups=5, min_launches=ch.k)[0] * 1e3
             del g
         for fused in (False, True):
             ch.fused = fused
             g = graph_of(ch.chain, torch)
-            step = time_replays([g], reps, 1, torch) * 1e3 / ch.k
+            tt = time_groups(g, ch.k, torch, groups=5, min_launches=ch.k)
+            step = tt[0] * 1e3
             del g
             out = {"config": f"C5 draft chain B={B} ctx 2048 k=6, neighbours "
                              + ("fused HIP kernels" if fused else "eager torch"),
-                   "step_us": round(step, 2), "attention_us": round(parts["attention"], 2),
+                   "step_us": round(step, 2),
+                   "step_minmax_us": [round(tt[1] * 1e3, 2), round(tt[2] * 1e3, 2)],
+                   "attention_us": round(parts["attention"], 2),
                    "gemv_us": round(parts["gemv"], 2),
                    "GBps": round(ch.step_bytes() / step / 1e3, 1),
                    "attention_share": round(parts["attention"] / step, 3),
@@ -651,14 +798,17 @@ def main():
     value = step_bytes / (ms_step * 1e-3) / 1e9
 
     # ---- dominant kernel: attention main kernel alone, HIP events on the launching
-    #      (current) stream around `steps` back-to-back graph replays
-    reps = max(1, args.steps // sets)
-    ms_main = time_replays(main_graphs, reps, max(1, args.warmup // sets), torch) / sets
-    ms_attn = time_replays(attn_graphs, reps, max(1, args.warmup // sets), torch) / sets
-    ms_floor = time_replays(floor_graphs, reps, max(1, args.warmup // sets), torch) / sets
-    ms_comb = time_replays(combine_graphs, reps, max(1, args.warmup // sets), torch) / sets
+    #      (current) stream around graph chains of back-to-back launches: the median
+    #      of 5 groups of >= 20 launches, whatever --steps is (min / max beside it)
+    t_main = time_groups(main_graphs[0], sets, torch)
+    t_attn = time_groups(attn_graphs[0], sets, torch)
+    t_floor = time_groups(floor_graphs[0], sets, torch)
+    t_comb = time_groups(combine_graphs[0], sets, torch)
+    ms_main, ms_attn, ms_floor, ms_comb = t_main[0], t_attn[0], t_floor[0], t_comb[0]
     a_bytes = attn_bytes(lens.tolist(), hq, hkv, d, 2)
     achieved = a_bytes / (ms_main * 1e-3) / 1e9
+    ceiling = read_ceiling(ops, torch)
+    ceiling["frac"] = round(achieved / ceiling["read_GBps"], 4)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -678,7 +828,13 @@ def main():
                      "traffic": load_traffic("paged_attn_main_c2_b32"),
                      "kernel": "paged_attn_main", "algorithmic_bytes": a_bytes,
                      "avg_us": round(ms_main * 1e3, 2),
+                     "avg_minmax_us": [round(t_main[1] * 1e3, 2), round(t_main[2] * 1e3, 2)],
+                     "timing": "median of 5 groups of >= 20 launches (graph chains over "
+                               f"{sets} page sets), HIP events on the launching stream",
                      "floor_us": round(ms_floor * 1e3, 2),
+                     "floor_minmax_us": [round(t_floor[1] * 1e3, 2),
+                                         round(t_floor[2] * 1e3, 2)],
+                     "ceiling": ceiling,
                      "floor_note": "sd_paged_attention_floor: the same grid, loads and "
                                    "prefetch with no math (the access pattern's time)",
                      "traffic_note": "bytes per launch from the committed rocprofv3 "
@@ -691,8 +847,11 @@ def main():
         del step_graphs, main_graphs, attn_graphs, step_chain, floor_graphs, combine_graphs
         del twin_ws
         extra = {"attention_op_us": round(ms_attn * 1e3, 2),
+                 "attention_op_minmax_us": [round(t_attn[1] * 1e3, 2), round(t_attn[2] * 1e3, 2)],
                  "attention_main_us": round(ms_main * 1e3, 2),
                  "attention_combine_us": round(ms_comb * 1e3, 2),
+                 "attention_combine_minmax_us": [round(t_comb[1] * 1e3, 2),
+                                                 round(t_comb[2] * 1e3, 2)],
                  "attention_floor_us": round(ms_floor * 1e3, 2),
                  "step_us": round(ms_step * 1e3, 2),
                  "step_us_one_graph_per_step": round(ms_step_graph * 1e3, 2)}
@@ -700,6 +859,8 @@ def main():
         torch.cuda.empty_cache()
         extra["decode_batches"] = [bench_decode_batch(ops, workloads, torch, b, args.steps)
                                    for b in (1, 8)]
+        torch.cuda.empty_cache()
+        extra["decode_ctx_sweep_b1"] = bench_ctx_sweep(ops, workloads, torch)
         torch.cuda.empty_cache()
         extra["verify"] = bench_verify(ops, workloads, torch, args.steps)
         torch.cuda.empty_cache()

@@ -129,8 +129,14 @@ int sd_paged_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
 /*
  * sd_paged_attention without the workspace arguments, allocating nothing: the
  * split-KV workspace is the library's static device scratch (one per device,
- * SD_NOALLOC_SCRATCH_BYTES, held from the first call on that device until the
- * process ends). No counterpart in the reference: it is for callers that cannot
+ * SD_NOALLOC_SCRATCH_BYTES). The scratch is part of the library's code
+ * object: it is reserved on every device where the library's kernels load,
+ * for any user of the library, whether or not this entry is ever called, and
+ * held until the process ends. Its device address is looked up once per
+ * device (hipGetSymbolAddress, on the first call with that device current)
+ * and kept: after hipDeviceReset, or anything else that reloads the library's
+ * code object on a device, that address is stale, and this entry must not be
+ * called again in the process. No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Same kernels, plan and results as
  * sd_paged_attention with a workspace (bit for bit). Sizes whose workspace
@@ -221,6 +227,21 @@ int sd_paged_attention_floor(const void* q, int64_t q_stride_tok, int64_t q_stri
                              int32_t num_splits, void* stream);
 
 /*
+ * The box's streaming-read ceiling: one grid-stride pass of 16-byte
+ * nontemporal loads over `bytes` (a positive multiple of 16) at `src`
+ * (16-byte aligned), with `workgroups` workgroups of 256 threads (<= 0: six
+ * per CU). Nothing is written except, practically never, one word of `sink`
+ * (4-byte aligned device memory), which keeps the loads alive. The bench
+ * divides the bytes by its time to get the bandwidth this GPU actually
+ * reaches, the second denominator beside the 8 TB/s data-sheet peak. No
+ * counterpart entry in the reference, which measured its own ceiling with a
+ * plain device copy (nanovllm/kernels/README.md:27-35); the kernels here read
+ * far more than they write, so the ceiling that bounds them is a read.
+ */
+int sd_stream_read(const void* src, int64_t bytes, void* sink, int32_t workgroups,
+                   void* stream);
+
+/*
  * store_kvcache + paged attention in one launch: the decode / verify layer call
  * `Attention.forward` (nanovllm/layers/attention.py:59-82: store_kvcache of the
  * new rows, then flash_attn_with_kvcache or the paged flash_attn_varlen_func).
@@ -273,9 +294,14 @@ size_t sd_w8a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_si
  * Dequantization is fused (int8 -> fp in registers, fp32 accumulation, scale
  * applied to the fp32 accumulator). One or two activation rows with a
  * per-channel scale on weights up to 32 MiB (M * ceil(K / 1024) <= 4) stream
- * whole weight rows through fp32 FMAs; other shapes run the MFMA kernel (the
- * SiLU and RMSNorm forms below follow the same rule). Supported: K % 64 == 0,
- * group_size 0 or a multiple of 64 dividing K. `workspace` may be NULL.
+ * whole weight rows through fp32 FMAs, and so does one row on larger weights
+ * (the lm_head), with batches of 4 rows dealt to the waves in turn; other
+ * shapes run the MFMA kernel (the SiLU and RMSNorm forms below follow the
+ * same rule). Supported: K % 64 == 0,
+ * group_size 0 or a multiple of 64 dividing K; N < 2^24 rows, a row stride
+ * below 2^24 bytes and N * w_stride_n < 2^32 bytes (the MFMA kernel forms a
+ * row's byte offset with one 24 x 24-bit multiply-add; SD_ERR_UNSUPPORTED
+ * otherwise). `workspace` may be NULL.
  * y may share no byte with x (SD_ERR_VALUE): other workgroups still read x
  * while one writes y.
  */
@@ -284,6 +310,22 @@ int sd_w8a16_linear(const void* x, int64_t x_stride_m, const int8_t* w, int64_t 
                     const void* bias, void* y, int64_t y_stride_m, int64_t M, int64_t N,
                     int64_t K, int32_t dtype, void* workspace, size_t workspace_bytes,
                     void* stream);
+
+/*
+ * Measurement twin of sd_w8a16_linear (per-channel scale): the same plan,
+ * grid, activation staging, weight loads and prefetch, with every loaded
+ * word folded into a register in place of the dequantization, the math and
+ * the epilogue. y is not written (a store guarded by a condition on the
+ * loaded data that is practically never true keeps the loads alive). Its time
+ * is what the kernel's access pattern alone costs. The W8A16 counterpart of
+ * sd_paged_attention_floor; the reference has no such twin for its int8
+ * kernel (its attention twin is paged_decode_readonly_kernel,
+ * nanovllm/kernels/paged_decode_attn_cuda.cu:654-705).
+ */
+int sd_w8a16_floor(const void* x, int64_t x_stride_m, const int8_t* w, int64_t w_stride_n,
+                   const void* scale, int32_t scale_dtype, const void* bias, void* y,
+                   int64_t y_stride_m, int64_t M, int64_t N, int64_t K, int32_t dtype,
+                   void* stream);
 
 /*
  * SiluAndMul fused into the W8A16 linear: y = (bf16(bf16(silu(g)) * u)) @

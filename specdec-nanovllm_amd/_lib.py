@@ -68,6 +68,12 @@ SIGNATURES = {
         _p, _i32, _p,                   # scale, scale_dtype, bias
         _p, _i64,                       # y, y_stride
         _i64, _i64, _i64, _i32, _p]),   # M, N, K, dtype, stream
+    "sd_stream_read": (ctypes.c_int, [_p, _i64, _p, _i32, _p]),  # src, bytes, sink, wgs, stream
+    "sd_w8a16_floor": (ctypes.c_int, [
+        _p, _i64, _p, _i64,             # x, x_stride, w, w_stride
+        _p, _i32, _p,                   # scale, scale_dtype, bias
+        _p, _i64,                       # y, y_stride
+        _i64, _i64, _i64, _i32, _p]),   # M, N, K, dtype, stream
     "sd_w8a16_linear": (ctypes.c_int, [
         _p, _i64, _p, _i64,             # x, x_stride, w, w_stride
         _p, _i32, _i32, _p,             # scale, scale_dtype, group_size, bias

@@ -1183,7 +1183,9 @@ constexpr int kMaxScratchDevices = 64;
 std::atomic<void*> g_scratch_addr[kMaxScratchDevices];
 
 // Device address of `scratch` on the current device, looked up once per
-// device (a racing second lookup stores the same address).
+// device (a racing second lookup stores the same address). A device reset
+// reloads the code object and leaves the kept address stale: the entry is
+// not for use after hipDeviceReset.
 int scratch_address(void** out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {

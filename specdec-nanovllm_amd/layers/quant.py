@@ -108,45 +108,65 @@ def int8_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
     return ops.w8a16_linear(x, qweight, scale, bias, gs)
 
 
+def _error_sample(w: torch.Tensor, q: torch.Tensor, s: torch.Tensor, granularity: str,
+                  group_size: int) -> float:
+    """Relative Frobenius error of the dequantized weight on its first 256
+    rows (a sample, so the check never expands a whole layer to fp32)."""
+    n = min(w.shape[0], 256)
+    ref = w[:n].float()
+    return ((ref - dequantize_weight(q[:n], s[:n], granularity, group_size)).norm()
+            / ref.norm()).item()
+
+
+def _swap_to_int8(name: str, mod: nn.Module, granularity: str, group_size: int) -> dict:
+    """Replace ``mod.weight`` (bf16) by its int8 form and a ``weight_scale``
+    parameter, set the two attributes ``LinearBase._apply`` dispatches on, and
+    describe what changed."""
+    w = mod.weight.data
+    q, s = quantize_weight(w, granularity, group_size)
+    frozen = dict(requires_grad=False)
+    mod.weight = nn.Parameter(q.to(w.device).contiguous(), **frozen)
+    mod.weight_scale = nn.Parameter(s.to(w.device).contiguous(), **frozen)
+    mod.quant_granularity, mod.quant_group_size = granularity, group_size
+    sf = s.float()
+    return dict(name=name, shape=list(w.shape),
+                rel_err=_error_sample(w, q, s, granularity, group_size),
+                saturate_frac=(q.abs() == QMAX).float().mean().item(),
+                scale_min=float(sf.min()), scale_max=float(sf.max()),
+                bytes_before=2 * w.numel(), bytes_after=q.numel() + 2 * s.numel())
+
+
 def apply_int8_quant(model: nn.Module, module_names, granularity: str = "per_channel",
                      group_size: int = 128, verbose: bool = False):
-    """Quantize the named ``LinearBase`` submodules of ``model`` in place.
+    """Quantize the named ``LinearBase`` submodules of ``model`` in place
+    (the contract of nanovllm/layers/quant.py:66-117).
 
     Each module's bf16 ``weight`` becomes an int8 parameter plus a
     ``weight_scale`` parameter, and ``quant_granularity``/``quant_group_size``
     are set, so ``LinearBase._apply`` dispatches to ``int8_linear``. Returns one
-    report dict per module (shape, relative error on up to 256 rows,
-    saturation fraction, scale range, bytes before/after).
+    report dict per module, in the model's module order (name, shape, relative
+    error on up to 256 rows, saturation fraction, scale range, bytes
+    before/after). Errors, as the reference raises them: ``KeyError`` for names
+    the model lacks, ``TypeError`` for a module that is not a ``LinearBase``,
+    ``AssertionError`` for a weight that is not bf16. Every module is checked
+    before any is changed, so a refused call leaves the model as it was.
     """
     from .linear import LinearBase
 
     wanted = set(module_names)
-    report = []
-    for name, mod in model.named_modules():
-        if name not in wanted:
-            continue
+    chosen = [(n, m) for n, m in model.named_modules() if n in wanted]
+    absent = wanted.difference(n for n, _ in chosen)
+    if absent:
+        raise KeyError(f"modules not found in the model: {sorted(absent)}")
+    for name, mod in chosen:
         if not isinstance(mod, LinearBase):
             raise TypeError(f"{name} is a {type(mod).__name__}, not a LinearBase")
-        w = mod.weight.data
-        assert w.dtype == torch.bfloat16, f"{name}: weight dtype {w.dtype} is not bf16"
-        q, s = quantize_weight(w, granularity, group_size)
-        mod.weight = nn.Parameter(q.to(w.device).contiguous(), requires_grad=False)
-        mod.weight_scale = nn.Parameter(s.to(w.device).contiguous(), requires_grad=False)
-        mod.quant_granularity = granularity
-        mod.quant_group_size = group_size
-        rows = min(w.shape[0], 256)
-        ref = w[:rows].to(torch.float32)
-        err = ref - dequantize_weight(q[:rows], s[:rows], granularity, group_size)
-        report.append({
-            "name": name, "shape": list(w.shape),
-            "rel_err": (err.norm() / ref.norm()).item(),
-            "saturate_frac": (q.abs() == QMAX).float().mean().item(),
-            "scale_min": float(s.float().min()), "scale_max": float(s.float().max()),
-            "bytes_before": w.numel() * 2, "bytes_after": q.numel() + s.numel() * 2,
-        })
-        if verbose:
-            print(f"  [int8] {name:<46} {tuple(w.shape)} rel_err={report[-1]['rel_err']:.5f}")
-    missing = wanted - {r["name"] for r in report}
-    if missing:
-        raise KeyError(f"modules not found in the model: {sorted(missing)}")
+        assert mod.weight.dtype == torch.bfloat16, \
+            f"{name}: weight dtype {mod.weight.dtype} is not bf16"
+    report = [_swap_to_int8(name, mod, granularity, group_size) for name, mod in chosen]
+    if verbose:
+        for r in report:
+            print(f"int8 {r['name']}: {r['shape'][0]}x{r['shape'][1]}, "
+                  f"rel err {r['rel_err']:.2e}, {r['bytes_before'] >> 10} -> "
+                  f"{r['bytes_after'] >> 10} KiB")
     return report

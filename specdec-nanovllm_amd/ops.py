@@ -273,12 +273,17 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 # -------------------------------------------------------------------------- w8a16
 def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
                  bias: torch.Tensor | None = None, group_size: int = 0,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
+                 out: torch.Tensor | None = None, twin: str | None = None) -> torch.Tensor:
     """y = x @ (qweight * scale)^T + bias with the dequantization fused.
 
     x: (..., K) fp16/bf16; qweight: (N, K) int8; scale: (N,) when
     ``group_size == 0`` else (N, K // group_size); returns (..., N) in x.dtype.
+    ``twin="floor"``: the measurement twin instead (sd_w8a16_floor: the same
+    plan, grid and loads with no math; per-channel scales only); the output
+    is left unwritten.
     """
+    if twin not in (None, "floor"):
+        raise ValueError(f"unknown twin {twin!r}")
     assert qweight.dtype == torch.int8, f"qweight must be int8, got {qweight.dtype}"
     assert qweight.dim() == 2
     N, K = qweight.shape
@@ -303,6 +308,17 @@ def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
     if M == 0:
         return y.view(*x.shape[:-1], N)
     lib = _lib.load()
+    if twin == "floor":
+        if group_size:
+            raise RuntimeError("w8a16 floor twin: per-channel scales only")
+        with torch.cuda.device(dev):
+            rc = lib.sd_w8a16_floor(
+                x2.data_ptr(), x2.stride(0), qw.data_ptr(), qw.stride(0),
+                sc.data_ptr(), _lib.dtype_code(sc.dtype), _ptr(b),
+                y.data_ptr(), y.stride(0), M, N, K, _lib.dtype_code(x.dtype),
+                _lib.stream_ptr(dev))
+        _lib.check(rc)
+        return y.view(*x.shape[:-1], N)
     ws_bytes = lib.sd_w8a16_workspace_size(M, N, K, int(group_size))
     ws = _workspace(ws_bytes, dev)
     with torch.cuda.device(dev):
@@ -757,3 +773,18 @@ def verify_batch(draft: torch.Tensor, target_logits: torch.Tensor, draft_tokens:
         if advance:
             rng_state[1:].add_(1)
     return accepted, bonus, mask
+
+
+# ---------------------------------------------------------------------- measurement
+def stream_read(buf: torch.Tensor, sink: torch.Tensor, workgroups: int = 0) -> None:
+    """One streaming read of ``buf`` (sd_stream_read): the box's read ceiling,
+    the bench's second denominator beside the 8 TB/s data-sheet peak.
+    ``sink``: at least one int32 of device memory, practically never written.
+    ``workgroups`` <= 0 takes the library's default (six per CU)."""
+    assert buf.is_contiguous() and sink.dtype == torch.int32 and sink.numel() >= 1
+    dev = _lib.require_device(buf, sink)
+    nbytes = buf.numel() * buf.element_size() // 16 * 16
+    with torch.cuda.device(dev):
+        rc = _lib.load().sd_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(),
+                                         int(workgroups), _lib.stream_ptr(dev))
+    _lib.check(rc)

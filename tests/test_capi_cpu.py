@@ -126,6 +126,8 @@ def test_ops_refuse_cpu_tensors():
                          torch.zeros((8, 64), dtype=torch.int8), torch.ones(8))
 
 
+@pytest.mark.skipif(torch.cuda.device_count() > 0,
+                    reason="fake device addresses: only where no GPU can be reached")
 def test_w8a16_rejects_overlapping_outputs():
     """Other workgroups still read x / residual while one writes y or
     residual_out, so any shared byte is refused before a launch."""
@@ -153,6 +155,25 @@ def test_w8a16_rejects_overlapping_outputs():
                                _lib.SD_BF16, None, 0, None) == _lib.SD_ERR_VALUE
     assert lib.sd_w8a16_silu_linear(x, 2 * K, w, K, s, _lib.SD_BF16, 0, None, x + 3 * row, N,
                                     M, N, K, _lib.SD_BF16, None) == _lib.SD_ERR_VALUE
+
+
+@pytest.mark.skipif(torch.cuda.device_count() > 0,
+                    reason="fake device addresses: only where no GPU can be reached")
+def test_w8a16_refuses_rows_past_24_bits():
+    """The tiled kernel forms a weight row's byte offset with one 24 x 24-bit
+    multiply-add, so 2^24 rows or more (even of a short row, under the 4 GiB
+    span) are refused before a launch; 2^24 - 16 rows pass the check."""
+    lib = _lib.load()
+    x, w, s, y = 0x100000, 0x200000, 0x300000, 0x40000000
+    K = 64
+    for N in ((1 << 24), (1 << 24) + 16):
+        rc = lib.sd_w8a16_linear(x, K, w, K, s, _lib.SD_F16, 0, None, y, N, 1, N, K,
+                                 _lib.SD_F16, None, 0, None)
+        assert rc == _lib.SD_ERR_UNSUPPORTED, N
+        assert b"2^24 rows" in lib.sd_last_error()
+    # the stride limit holds on its own too
+    assert lib.sd_w8a16_linear(x, 1 << 24, w, 1 << 24, s, _lib.SD_F16, 0, None, y, 16, 1, 16,
+                               K, _lib.SD_F16, None, 0, None) == _lib.SD_ERR_UNSUPPORTED
 
 
 # ------------------------------------------------------------------ argument sweep

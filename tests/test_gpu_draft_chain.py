@@ -8,8 +8,9 @@ Both forms of the step are covered: eager-torch neighbours and this library's
 fused neighbour kernels — on a small stack (every step checked), and at the C5
 configuration itself (28 layers, hidden 1024, 16 q / 8 kv heads, intermediate
 3072, vocab 151936, a 2048-token context prefilled from uniform random token
-ids, k = 6 steps, batch 1 and 16: step 0 checked against the reference, every
-drafted token against the argmax of its logits, the graph replay bitwise).
+ids, k = 6 steps, batch 1 and 16: the first and the last step checked against
+the reference, every drafted token against the argmax of its logits, the graph
+replay bitwise).
 """
 import pytest
 import torch
@@ -153,6 +154,15 @@ def test_c5_configuration(c5_chain, fused):
     ref = ref_step(ch, kv_ref, tok0[0], 0)
     err = (logits[0] - ref).abs().max().item()
     assert err <= 2e-2 * ref.abs().max().item(), f"step 0: max err {err:.4g}"
+    # the last draft step (s = k - 1) against the reference too, over the cache
+    # the chain's own steps 0 .. k - 2 left (their rows are in eager_kv; the
+    # reference rewrites step k - 1's rows itself)
+    last = ch.k - 1
+    print(f"C5 chain B={ch.B} fused={fused}: float32 reference of step {last}", flush=True)
+    kv_ref = eager_kv.clone()
+    ref = ref_step(ch, kv_ref, eager_tok[last], last)
+    err = (logits[last] - ref).abs().max().item()
+    assert err <= 2e-2 * ref.abs().max().item(), f"step {last}: max err {err:.4g}"
     del kv_ref, ref, logits
     print(f"C5 chain B={ch.B} fused={fused}: HIP graph of the 6 steps", flush=True)
     ch.kv.copy_(kv0)

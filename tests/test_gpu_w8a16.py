@@ -164,7 +164,8 @@ def test_errors():
                                           (56, 1024, 3072, 0, torch.bfloat16),
                                           (3, 33000, 1024, 0, torch.bfloat16),
                                           (20, 33000, 1024, 128, torch.float16),
-                                          (40, 33000, 1024, 0, torch.bfloat16)])
+                                          (40, 33000, 1024, 0, torch.bfloat16),
+                                          (1, 16411, 2048, 0, torch.bfloat16)])
 def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
     # the down projection fed straight from gate_up (narrow K-split path and the
     # wide path with staged activations): bit-identical to the two-launch form
@@ -197,7 +198,9 @@ def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
                                               (2, 1024, 8192, 0, torch.bfloat16, False),
                                               (9, 33000, 1024, 128, torch.float16, True),
                                               (24, 33000, 1024, 0, torch.bfloat16, True),
-                                              (48, 33000, 1024, 0, torch.bfloat16, True)])
+                                              (48, 33000, 1024, 0, torch.bfloat16, True),
+                                              (1, 151936, 1024, 0, torch.bfloat16, True),
+                                              (1, 16411, 2048, 0, torch.float16, False)])
 def test_rmsnorm_linear_is_rmsnorm_then_linear(M, N, K, gs, act, res):
     # add + RMSNorm formed while staging: bit-identical to rmsnorm then the
     # linear, residual_out identical to rmsnorm's (one row block per 16 or 32
@@ -278,10 +281,9 @@ def test_row_streaming_path(M, K, gs, act):
     # one or two activation rows at small K with a per-channel scale take the
     # row-streaming kernel (whole 1 KB weight rows per load, activations in
     # registers): bias, a partial last 1024-column chunk (K = 2560), N not a
-    # multiple of the rows per wave; the per-group cases check the tiled kernel
-    # at the same shapes
-    if M * ((K + 1023) // 1024) > 4:
-        pytest.skip("this M x K takes the tiled kernel")
+    # multiple of the rows per wave. The per-group cases, and two rows past
+    # M * ceil(K / 1024) = 4 (K = 3072, 4096), check the tiled kernel on the
+    # other side of the dispatch rule at the same shapes.
     N = 3001
     c = workloads.w8a16_case(M, N, K, seed=K + M, act_dtype=act)
     g = workloads.device_generator(DEV, K + 7)
@@ -347,3 +349,65 @@ def test_gate_up_silu_entry_refuses_shapes_off_its_paths():
                                    _lib.dtype_code(c["s"].dtype), None, y.data_ptr(), y.stride(0),
                                    3, 2064, 1024, _lib.SD_F16, _lib.stream_ptr(torch.device(DEV)))
     assert rc == _lib.SD_ERR_UNSUPPORTED and b"row-streaming" in lib.sd_last_error()
+
+
+# ------------------------------------------------- wide matrices at one row
+@pytest.mark.parametrize("N,K", [(151936, 1024), (16411, 2048), (32771, 1024), (8209, 4096)])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_batch_cyclic_rows_on_wide_matrices(N, K, act):
+    # one activation row on more than 32 MiB of weights takes the row kernel
+    # with batches of 4 rows dealt to the waves in turn: N not a multiple of
+    # the batch, of the waves, or of 16; 1 - 4 column chunks; bias
+    assert N * K > 32 << 20
+    c = workloads.w8a16_case(1, N, K, seed=N + K, act_dtype=act)
+    g = workloads.device_generator(DEV, N)
+    bias = torch.randn((N,), generator=g, device=DEV).to(act)
+    y = ops.w8a16_linear(c["x"], c["w"], c["s"], bias)
+    check(y, c["x"], c["w"], c["s"], bias,
+          out_rel=2.0 ** -9 if act == torch.float16 else 2.0 ** -8, what=f"cyclic N={N} K={K}")
+    # every output written exactly once: a second call into a NaN-filled
+    # buffer gives the same bits
+    out = torch.full_like(y, float("nan"))
+    ops.w8a16_linear(c["x"], c["w"], c["s"], bias, out=out)
+    assert torch.equal(out, y)
+
+
+def test_two_rows_on_wide_matrices_stay_on_the_tiled_kernel():
+    # M = 2 past 32 MiB is not a row-kernel shape: same tolerance via the tiled path
+    c = workloads.w8a16_case(2, 151936, 1024, seed=2)
+    check(ops.w8a16_linear(c["x"], c["w"], c["s"]), c["x"], c["w"], c["s"], what="M=2 lm_head")
+
+
+# ----------------------------------------------------- measurement twins
+@pytest.mark.parametrize("M,N,K", [(1, 151936, 1024), (7, 151936, 1024), (56, 151936, 1024),
+                                   (1, 4096, 1024), (16, 1024, 3072), (56, 6144, 1024)])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_floor_twin_runs_the_plan_and_writes_nothing(M, N, K, act):
+    # sd_w8a16_floor: the same plan with no math leaves the output untouched
+    # (its store is guarded by a condition on the loaded data that these
+    # inputs never meet) and leaves the real call's result unchanged after it
+    c = workloads.w8a16_case(M, N, K, seed=M + N, act_dtype=act)
+    sentinel = torch.full((M, N), 7.0, dtype=act, device=DEV)
+    out = sentinel.clone()
+    ops.w8a16_linear(c["x"], c["w"], c["s"], out=out, twin="floor")
+    torch.cuda.synchronize()
+    assert torch.equal(out, sentinel)
+    y = ops.w8a16_linear(c["x"], c["w"], c["s"])
+    check(y, c["x"], c["w"], c["s"], out_rel=2.0 ** -9 if act == torch.float16 else 2.0 ** -8,
+          what=f"after floor M={M} N={N}")
+    with pytest.raises(RuntimeError, match="per-channel"):
+        ops.w8a16_linear(c["x"], c["w"], torch.ones((N, K // 128), device=DEV, dtype=act),
+                         group_size=128, twin="floor")
+
+
+def test_stream_read_ceiling_reads_and_writes_nothing():
+    buf = torch.randint(0, 255, (64 << 20,), dtype=torch.uint8, device=DEV)
+    sink = torch.full((4,), 5, dtype=torch.int32, device=DEV)
+    for wg in (0, 256, 1536):
+        ops.stream_read(buf, sink, wg)
+    torch.cuda.synchronize()
+    assert sink.tolist() == [5, 5, 5, 5]
+    lib = _lib.load()
+    assert lib.sd_stream_read(buf.data_ptr(), 15, sink.data_ptr(), 0, None) == _lib.SD_ERR_VALUE
+    assert lib.sd_stream_read(buf.data_ptr() + 8, 1024, sink.data_ptr(), 0,
+                              None) == _lib.SD_ERR_VALUE
