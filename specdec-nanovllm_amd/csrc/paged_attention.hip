@@ -60,7 +60,7 @@ using sd::f32x4;
 using sd::u32x4;
 
 constexpr int kD = 128;                // head_dim
-constexpr int kThreads = 256;          // combine kernel
+constexpr int kCombThreads = 256;      // most threads of a combine workgroup (8 groups of 32)
 constexpr int kStep = 32;              // keys of one wave's share of a column
 constexpr int kKPitch = 136;  // 16-bit elements per LDS row of a K tile (272 B: b128 reads of
                               // 16 consecutive rows hit distinct banks)
@@ -97,7 +97,8 @@ struct AttnParams {
   int32_t runs;
   int32_t min_steps;  // lower bound of columns per run
   int32_t col_keys;   // keys per column: 32 KS (KS waves per kv head)
-  int32_t comb_rows;  // query rows per combine workgroup (a power of two <= 8)
+  int32_t comb_rows;    // query rows per combine workgroup (a power of two)
+  int32_t comb_slices;  // groups of 32 threads per row, each merging a share of its partials
   int32_t rmax;       // G * max_qlen
   // Fused store_kvcache (knew == NULL: none). Query row t's key/value row is
   // knew/vnew row t; sequence b's rows are its last n_b keys.
@@ -824,11 +825,16 @@ __device__ void cols_split(const AttnParams& p, int b, int& before, int& total) 
 }
 
 // Log-sum-exp merge of the partials of pair (b, h) = (blockIdx.z, blockIdx.y),
-// rows blockIdx.x * rpw .. + rpw (rpw = comb_rows, a power of two <= 8), zero
-// rows for sequences without keys. The 8 groups of 32 threads (4 dims per
-// thread) are rpw rows x 8 / rpw slices: slice s of a row merges its own
-// contiguous share of the row's partials, all loads of a batch in flight at
-// once, then slice 0 merges the slices' states (LDS) in slice order. Sequence
+// rows blockIdx.x * rpw .. + rpw (rpw = comb_rows), zero rows for sequences
+// without keys. The workgroup is rpw rows x nsl slices x 32 threads (4 dims per
+// thread; one slice where the plan expects at most 16 partials per pair, else
+// 8 / rpw): slice s of a row merges its own contiguous share of the row's
+// partials, all loads of a batch in flight at once, then (nsl > 1) slice 0
+// merges the slices' states (LDS) in slice order. The merge arithmetic runs
+// for the partials that exist only (a batch's unrolled steps past the slice's
+// count are skipped), in the exp2 domain with the native v_exp_f32: a slice that
+// ran all 16 steps under predicates, with the library exp2f, spent about 1 us
+// on them. Sequence
 // b spans columns [f, f + n); the runs that met it are f / S .. (f + n - 1) / S
 // and run r's wave of head h wrote its partial to slot
 // (r + b) * Hkv + h. Without STORE a pair met by one run is already final.
@@ -842,7 +848,7 @@ template <typename T, bool STORE>
 __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   constexpr int kBatch = 16;   // partial loads in flight per thread
   constexpr int kNewMax = 8;   // new rows whose loads are issued up front
-  constexpr int kGroups = kThreads / 32;
+  constexpr int kGroups = kCombThreads / 32;
   __shared__ __attribute__((aligned(16))) float4 s_o[kGroups][32];
   __shared__ float2 s_ml[kGroups];
   const int h = blockIdx.y, b = blockIdx.z;
@@ -859,7 +865,7 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
     cols_split<STORE>(p, b, f, total);
   }
   const int grp = threadIdx.x >> 5, d4 = (threadIdx.x & 31) * 4;
-  const int rpw = p.comb_rows, nsl = kGroups / rpw;
+  const int rpw = p.comb_rows, nsl = p.comb_slices;
   const int sl = grp / rpw;
   const int row = blockIdx.x * rpw + grp % rpw;
   const int qi = row / p.G, g = row - qi * p.G;
@@ -915,16 +921,18 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
         }
         float mc = M;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) mc = fmaxf(mc, part[u].x);
+        for (int u = 0; u < kBatch; ++u) mc = fmaxf(mc, part[u].x);  // -inf past the count
         if (mc == -INFINITY) continue;
-        const float r = exp2f(M - mc);  // rescale what earlier batches summed
+        const float r = sd::fast_exp2(M - mc);  // rescale what earlier batches summed
         l *= r;
         o *= r;
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
-          const float w = exp2f(part[u].x - mc);
-          l += w * part[u].y;
-          o += w * a[u];
+          if (c0 + u < u1) {  // false on the whole wave past the slice's count: skipped
+            const float w = sd::fast_exp2(part[u].x - mc);
+            l += w * part[u].y;
+            o += w * a[u];
+          }
         }
         M = mc;
       }
@@ -938,13 +946,13 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
       float mc = M;
       for (int s2 = 1; s2 < nsl; ++s2) mc = fmaxf(mc, s_ml[s2 * rpw + grp].x);
       if (mc != -INFINITY) {
-        const float r = exp2f(M - mc);
+        const float r = sd::fast_exp2(M - mc);
         l *= r;
         o *= r;
         for (int s2 = 1; s2 < nsl; ++s2) {
           const float2 pm = s_ml[s2 * rpw + grp];
           const float4 po = s_o[s2 * rpw + grp][threadIdx.x & 31];
-          const float w = exp2f(pm.x - mc);
+          const float w = sd::fast_exp2(pm.x - mc);
           l += w * pm.y;
           o += w * f32x4{po.x, po.y, po.z, po.w};
         }
@@ -973,7 +981,7 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
       for (int off = 1; off < 32; off <<= 1) dot += __shfl_xor(dot, off);
       const float sj = dot * p.scale_log2;
       const float mn = fmaxf(M, sj);
-      const float r = exp2f(M - mn), w = exp2f(sj - mn);
+      const float r = sd::fast_exp2(M - mn), w = sd::fast_exp2(sj - mn);
       l = l * r + w;
       o = o * r + w * vv;
       M = mn;
@@ -1008,7 +1016,7 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
         if (!use[j]) continue;
         const float sj = dot[j] * p.scale_log2;
         const float mn = fmaxf(M, sj);
-        const float r = exp2f(M - mn), w = exp2f(sj - mn);
+        const float r = sd::fast_exp2(M - mn), w = sd::fast_exp2(sj - mn);
         l = l * r + w;
         o = o * r + w * vn[j];
         M = mn;
@@ -1028,14 +1036,14 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
 
 // STORE: the launch's share of the fused store (grid-stride over the pieces).
 template <typename T, bool STORE>
-__global__ __launch_bounds__(kThreads) void paged_attn_combine(AttnParams p) {
+__global__ __launch_bounds__(kCombThreads) void paged_attn_combine(AttnParams p) {
   if constexpr (!STORE) {
     combine_rows<T, false>(p);
   } else {
     const uint32_t items = 2u * static_cast<uint32_t>(p.total_q) * p.Hkv * (kD * 2 / 16);
-    const uint32_t nthreads = gridDim.x * gridDim.y * gridDim.z * kThreads;
+    const uint32_t nthreads = gridDim.x * gridDim.y * gridDim.z * blockDim.x;
     const uint32_t it0 =
-        ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * kThreads + threadIdx.x;
+        ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
     StorePiece sp;
     if (it0 < items) {
       piece_of(p, it0, sp);
@@ -1061,6 +1069,8 @@ struct Plan {
   int nwg;        // workgroups of the main grid: runs * Hkv / NW
   int min_steps;  // lower bound of columns per run
   int rmax;       // rows per (sequence, kv head) in the workspace
+  int comb_rows;  // combine workgroup: rows x slices x 32 threads
+  int comb_slices;
   int64_t slots;  // partial slots: (runs + num_seqs) * Hkv
 };
 
@@ -1099,6 +1109,18 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   pl.runs = static_cast<int>(runs);
   pl.nwg = static_cast<int>(runs * groups);
   pl.slots = (runs + num_seqs) * Hkv;
+  // Combine workgroup: a power of two of rows covering G * max_qlen (at most 8),
+  // each row's partials split over the rest of 8 groups of 32 threads. A pair
+  // meets about runs / num_seqs + 1 runs; where one slice can merge that many in
+  // one batch of 16 (1.5 x the mean, plus 2: decode from about 12 sequences)
+  // the row keeps one slice and the workgroup shrinks, with no LDS merge (C2
+  // B = 32 combine 4.4 -> 4.1 us; more slices than 8 groups allow measured
+  // slower for one sequence and for verify).
+  pl.comb_rows = 1;
+  while (pl.comb_rows < 8 && pl.comb_rows < pl.rmax) pl.comb_rows *= 2;
+  const int64_t ns = num_seqs;
+  const int64_t est = (3 * runs + 2 * ns - 1) / (2 * ns) + 2;
+  pl.comb_slices = est <= 16 ? 1 : 8 / pl.comb_rows;
   return pl;
 }
 
@@ -1156,10 +1178,11 @@ int launch_all(const AttnParams& p, const Plan& pl, RunMode mode, hipStream_t st
     if (rc != SD_OK || mode == kRunMain) return rc;
   }
   const dim3 grid((pl.rmax + p.comb_rows - 1) / p.comb_rows, p.Hkv, p.num_seqs);
+  const dim3 block(static_cast<unsigned>(p.comb_rows * p.comb_slices * 32));
   if (p.knew)
-    hipLaunchKernelGGL((paged_attn_combine<T, true>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((paged_attn_combine<T, true>), grid, block, 0, st, p);
   else
-    hipLaunchKernelGGL((paged_attn_combine<T, false>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((paged_attn_combine<T, false>), grid, block, 0, st, p);
   return sd::check_launch("paged_attention combine");
 }
 
@@ -1345,10 +1368,8 @@ int run_attention(RunMode mode, const NewRows& nr, const void* q, int64_t q_stri
   p.runs = pl.runs;
   p.min_steps = pl.min_steps;
   p.col_keys = kStep * pl.KS;
-  // rows per combine workgroup: few rows (decode) leave groups free to split
-  // each row's partials
-  p.comb_rows = 1;
-  while (p.comb_rows < 8 && p.comb_rows < pl.rmax) p.comb_rows *= 2;
+  p.comb_rows = pl.comb_rows;
+  p.comb_slices = pl.comb_slices;
   p.knew = static_cast<const uint16_t*>(nr.key);
   p.vnew = static_cast<const uint16_t*>(nr.value);
   p.kn_stok = nr.key_stride_tok;

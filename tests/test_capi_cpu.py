@@ -208,6 +208,9 @@ PLAUSIBLE = {
     "sd_prefill_attention": {1: 4096, 2: 128, 5: 1024, 6: 128, 7: 256 * 1024, 8: 64, 9: 256,
                              11: 16, 12: 16, 15: 64, 16: 1024, 17: 16, 18: 32, 19: 8,
                              20: 128, 22: 0, 24: 4096, 25: 128},
+    # no dtype to leave invalid: two bad arguments (a ragged byte count, a misaligned
+    # sink), so that no single mutation reaches a launch on a host without a GPU
+    "sd_stream_read": {1: 15, 2: 0x10000001},
 }
 
 
