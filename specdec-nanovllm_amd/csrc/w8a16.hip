@@ -611,117 +611,14 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
   }
 }
 
-// ---- row-streaming GEMV for one or two activation rows (decode)
-// Each wave owns a contiguous range of weight rows and streams them whole: a
-// load instruction moves 1 KB of one row (lane l: bytes 16 l .. +16 of each
-// 1024-column chunk), R rows per batch, two batches in flight. Lane l holds
-// the activations of its columns (MR rows x C chunks x 16) in registers for
-// the whole launch, formed once per wave: MODE 1 SiluAndMul (silu_mul8, the
-// SiLU kernel's element function), MODE 2 add + RMSNorm with the RMSNorm
-// kernel's summation order (below), so the fused forms equal their two-launch
-// forms bit for bit. Products accumulate in fp32 per lane (one conversion and
-// one FMA per weight), then the R x MR sums of a batch reduce across the
-// lanes in one reduce-scatter (halving steps, then plain xor steps), so a
-// row's result is always summed in the same order. No MFMA, no LDS: at a few
-// rows the MFMA form spends its time on operand staging, not on math.
-// Per-channel scales only (applied to the reduced sum).
-template <int MR, int C, int R>
-struct RowsShape {
-  static constexpr int V = R * MR;  // sums per lane per batch (R: rows of a batch)
-  static constexpr int LV = V == 16 ? 4 : (V == 8 ? 3 : (V == 4 ? 2 : (V == 2 ? 1 : 0)));
-  static_assert((1 << LV) == V, "R * MR must be a power of two <= 16");
-};
-
-// PAIR (the gate_up projection with SiluAndMul, sd_w8a16_gate_up_silu): a
-// wave owns output columns i (weight rows i and i + p.pair); a batch holds
-// R / 2 gate rows then the R / 2 matching up rows. After the reduce-scatter
-// the gate sum of a pair sits 32 lanes below its up sum, so one xor-32
-// shuffle brings them together and the lower lane writes
-// bf16(bf16(silu(g)) * u) of the two bf16-rounded sums — the bits that the
-// linear followed by the SiLU kernel give.
-//
-// CYC (wide matrices): batches of R rows are dealt to the waves in turn, wave
-// w taking batches w, w + W, w + 2 W, ... (W waves in the grid), so at any
-// moment the waves stream neighbouring rows and each batch is R whole rows of
-// contiguous bytes. Contiguous ranges of ~75 rows per wave left the lm_head
-// (151936 x 1024) at 29.3 - 31.3 us against 26.6 - 26.9 us this way (same
-// box; the tiled MFMA kernel 29.9).
-// FLOOR: the measurement twin — the same grid, loads and prefetch, every
-// loaded word folded into a register instead of the math, no output.
-template <typename T, int MR, int C, int R, int MODE, bool PAIR = false, bool CYC = false,
-          bool FLOOR = false>
-__global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int rows_per_wave) {
-#pragma clang fp contract(off)
-  constexpr int V = RowsShape<MR, C, R>::V, LV = RowsShape<MR, C, R>::LV;
-  constexpr int RP = PAIR ? R / 2 : R;  // output rows (pairs) per batch
-  static_assert(!PAIR || (R % 2 == 0 && V / 2 * (64 >> LV) == 32), "pairs 32 lanes apart");
-  static_assert(!(PAIR && CYC), "paired rows run on narrow layers only");
-  const int lane = threadIdx.x & 63;
-  const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  // batches of this wave: nbat of them, the j-th starting at output row base(j);
-  // rows at or past r1 are clamped on load and never written
-  int r0, r1, nbat;
-  if constexpr (CYC) {
-    const int nb = (p.N + RP - 1) / RP;
-    const int W = gridDim.x * kWaves;
-    r0 = gw * RP;
-    r1 = p.N;
-    nbat = gw < nb ? (nb - gw + W - 1) / W : 0;
-  } else {
-    r0 = gw * rows_per_wave;
-    r1 = min(r0 + rows_per_wave, p.N);
-    nbat = r0 < p.N ? (r1 - r0 + RP - 1) / RP : 0;
-  }
-  if (nbat == 0) return;
-  auto base = [&](int j) {
-    return CYC ? (gw + j * static_cast<int>(gridDim.x) * kWaves) * RP : r0 + j * RP;
-  };
-
-  // weight row of batch row r for the output rows starting at rb
-  auto wrow = [&](int rb, int r) -> int64_t {
-    const int64_t o = min(rb + (PAIR ? r % RP : r), r1 - 1);
-    return PAIR && r >= RP ? o + p.pair : o;
-  };
-  // ---- a batch: R weight rows, and the scale (and bias) of the row whose sum
-  // this lane holds after the reduce-scatter, loaded together so that using
-  // them never waits for the next batch's prefetch (vector loads complete in
-  // order). The scale is read as 16-bit halves at a uniform shift (two halves
-  // of an fp32 scale, or one 16-bit scale twice) and the bias from the scale
-  // when there is none: one load form for every dtype, no branch.
-  struct Batch {
-    u32x4 w[R][C];
-    uint32_t s0, s1, b;
-  };
-  const int srow = (lane >> (6 - LV)) / MR;  // batch row of this lane's sum
-  const int ssh = p.scale_dtype == SD_F32 ? 1 : 0;
-  const uint16_t* s16 = static_cast<const uint16_t*>(p.scale);
-  const uint16_t* bsrc = p.bias ? p.bias : s16;
-  const int64_t bmask = p.bias ? ~int64_t{0} : int64_t{0};
-  auto load = [&](Batch& B, int rb) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t row = wrow(rb, r);
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        const int k0 = min(c * 1024 + 16 * lane, p.K - 16);  // lanes past K: a valid address, unused
-        B.w[r][c] = sd::load16_stream(p.w + row * p.ws + k0);
-      }
-    }
-    const int64_t row = wrow(rb, srow);
-    B.s0 = s16[row << ssh];
-    B.s1 = s16[(row << ssh) + ssh];
-    B.b = bsrc[row & bmask];
-  };
-  auto scale_of = [&](const Batch& B) -> float {
-    if (ssh) return __uint_as_float(B.s0 | (B.s1 << 16));
-    const uint16_t h = static_cast<uint16_t>(B.s0);
-    return p.scale_dtype == SD_BF16 ? sd::from_bits<__bf16>(h) : sd::from_bits<_Float16>(h);
-  };
-  Batch ba, bb;
-  load(ba, base(0));  // before the activations, so that their latencies overlap
-
-  // ---- this lane's activations: xv[m][c][j] = column c * 1024 + 16 lane + j
-  float xv[MR][C][16];
+// Lane `lane`'s activations of the row-streaming kernels: xv[m][c][j] is column
+// c * 1024 + 16 lane + j of activation row m (zero past K or M). MODE 1 forms
+// SiluAndMul (silu_mul8, the SiLU kernel's element function), MODE 2 add +
+// RMSNorm with the RMSNorm kernel's summation order; `writer` (one wave of
+// the grid) stores the new residual.
+template <typename T, int MR, int C, int MODE>
+__device__ __forceinline__ void row_activations(const W8Params& p, int lane, bool writer,
+                                                float (&xv)[MR][C][16]) {
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     const bool mok = m < p.M;
@@ -759,7 +656,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
               xv[m][c][8 * e + i] = f;
               ss[c & 1][e] += f * f;
             }
-            if (p.nres_out && gw == 0 && mok) {
+            if (p.nres_out && writer && mok) {
               uint32_t ro[4];
 #pragma unroll
               for (int i = 0; i < 4; ++i) ro[i] = sd::pack2<T>(xv[m][c][8 * e + 2 * i], xv[m][c][8 * e + 2 * i + 1]);
@@ -823,6 +720,100 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
       }
     }
   }
+}
+
+// ---- row-streaming GEMV for one or two activation rows (decode)
+// Each wave owns a contiguous range of weight rows and streams them whole: a
+// load instruction moves 1 KB of one row (lane l: bytes 16 l .. +16 of each
+// 1024-column chunk), R rows per batch, two batches in flight. Lane l holds
+// the activations of its columns (MR rows x C chunks x 16) in registers for
+// the whole launch, formed once per wave: MODE 1 SiluAndMul (silu_mul8, the
+// SiLU kernel's element function), MODE 2 add + RMSNorm with the RMSNorm
+// kernel's summation order (below), so the fused forms equal their two-launch
+// forms bit for bit. Products accumulate in fp32 per lane (one conversion and
+// one FMA per weight), then the R x MR sums of a batch reduce across the
+// lanes in one reduce-scatter (halving steps, then plain xor steps), so a
+// row's result is always summed in the same order. No MFMA, no LDS: at a few
+// rows the MFMA form spends its time on operand staging, not on math.
+// Per-channel scales only (applied to the reduced sum).
+template <int MR, int C, int R>
+struct RowsShape {
+  static constexpr int V = R * MR;  // sums per lane per batch (R: rows of a batch)
+  static constexpr int LV = V == 16 ? 4 : (V == 8 ? 3 : (V == 4 ? 2 : (V == 2 ? 1 : 0)));
+  static_assert((1 << LV) == V, "R * MR must be a power of two <= 16");
+};
+
+// PAIR (the gate_up projection with SiluAndMul, sd_w8a16_gate_up_silu): a
+// wave owns output columns i (weight rows i and i + p.pair); a batch holds
+// R / 2 gate rows then the R / 2 matching up rows. After the reduce-scatter
+// the gate sum of a pair sits 32 lanes below its up sum, so one xor-32
+// shuffle brings them together and the lower lane writes
+// bf16(bf16(silu(g)) * u) of the two bf16-rounded sums — the bits that the
+// linear followed by the SiLU kernel give.
+// FLOOR: the measurement twin — the same grid, loads and prefetch, every
+// loaded word folded into a register instead of the math, no output.
+template <typename T, int MR, int C, int R, int MODE, bool PAIR = false, bool FLOOR = false>
+__global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int rows_per_wave) {
+#pragma clang fp contract(off)
+  constexpr int V = RowsShape<MR, C, R>::V, LV = RowsShape<MR, C, R>::LV;
+  constexpr int RP = PAIR ? R / 2 : R;  // output rows (pairs) per batch
+  static_assert(!PAIR || (R % 2 == 0 && V / 2 * (64 >> LV) == 32), "pairs 32 lanes apart");
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  // batches of this wave: nbat of them, the j-th starting at output row base(j);
+  // rows at or past r1 are clamped on load and never written
+  const int r0 = gw * rows_per_wave;
+  const int r1 = min(r0 + rows_per_wave, p.N);
+  const int nbat = r0 < p.N ? (r1 - r0 + RP - 1) / RP : 0;
+  if (nbat == 0) return;
+  auto base = [&](int j) { return r0 + j * RP; };
+
+  // weight row of batch row r for the output rows starting at rb
+  auto wrow = [&](int rb, int r) -> int64_t {
+    const int64_t o = min(rb + (PAIR ? r % RP : r), r1 - 1);
+    return PAIR && r >= RP ? o + p.pair : o;
+  };
+  // ---- a batch: R weight rows, and the scale (and bias) of the row whose sum
+  // this lane holds after the reduce-scatter, loaded together so that using
+  // them never waits for the next batch's prefetch (vector loads complete in
+  // order). The scale is read as 16-bit halves at a uniform shift (two halves
+  // of an fp32 scale, or one 16-bit scale twice) and the bias from the scale
+  // when there is none: one load form for every dtype, no branch.
+  struct Batch {
+    u32x4 w[R][C];
+    uint32_t s0, s1, b;
+  };
+  const int srow = (lane >> (6 - LV)) / MR;  // batch row of this lane's sum
+  const int ssh = p.scale_dtype == SD_F32 ? 1 : 0;
+  const uint16_t* s16 = static_cast<const uint16_t*>(p.scale);
+  const uint16_t* bsrc = p.bias ? p.bias : s16;
+  const int64_t bmask = p.bias ? ~int64_t{0} : int64_t{0};
+  auto load = [&](Batch& B, int rb) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = wrow(rb, r);
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int k0 = min(c * 1024 + 16 * lane, p.K - 16);  // lanes past K: a valid address, unused
+        B.w[r][c] = sd::load16_stream(p.w + row * p.ws + k0);
+      }
+    }
+    const int64_t row = wrow(rb, srow);
+    B.s0 = s16[row << ssh];
+    B.s1 = s16[(row << ssh) + ssh];
+    B.b = bsrc[row & bmask];
+  };
+  auto scale_of = [&](const Batch& B) -> float {
+    if (ssh) return __uint_as_float(B.s0 | (B.s1 << 16));
+    const uint16_t h = static_cast<uint16_t>(B.s0);
+    return p.scale_dtype == SD_BF16 ? sd::from_bits<__bf16>(h) : sd::from_bits<_Float16>(h);
+  };
+  Batch ba, bb;
+  load(ba, base(0));  // before the activations, so that their latencies overlap
+
+  // ---- this lane's activations: xv[m][c][j] = column c * 1024 + 16 lane + j
+  float xv[MR][C][16];
+  row_activations<T, MR, C, MODE>(p, lane, gw == 0, xv);
 
   u32x4 fold = {0u, 0u, 0u, 0u};  // FLOOR: every loaded word is consumed here
   auto consume = [&](const Batch& B, int rb) {
@@ -912,6 +903,185 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
       for (int c = 0; c < C; ++c)
 #pragma unroll
         for (int i = 0; i < 16; ++i) xs += xv[m][c][i];
+    const uint32_t f = fold.x ^ fold.y ^ fold.z ^ fold.w ^ __float_as_uint(xs);
+    if (f == 0x9E3779B9u && lane == 0) p.y[0] = static_cast<uint16_t>(f);
+  }
+}
+
+// ---- row-cyclic GEMV for one activation row on wide matrices (the lm_head)
+// Weight row n belongs to wave n % W (W waves in the grid), so at any moment the
+// grid streams one window of neighbouring rows, and each wave keeps two whole
+// rows (C KB each) in flight: the load of row j + 2 is issued once row j has
+// arrived (its address takes a zero computed from row j's data), then row j is
+// computed. On a 151936 x 1024 matrix one or two 1 KB loads in flight per wave
+// at 12 - 24 waves per CU read at the streaming rate (6.9 TB/s); four or more
+// per wave (batches of contiguous rows) reached 5.5 - 6.5 TB/s.
+// Workgroups are renumbered so that each XCD (hardware blocks b with equal
+// b % 8) runs consecutive numbers: the 64 outputs of a 128-byte line of y, and
+// the line of scales beside them, then belong to one XCD's L2 instead of
+// eight (27.1 -> 25.8 us in the probe that chose this form).
+// Four rows' sums reduce across the lanes with two lane-half swaps
+// (v_permlane32_swap, v_permlane16_swap) and four DPP adds, without LDS; the
+// scales (and bias) of a wave's next 64 rows are gathered once, one row per
+// lane, and read back with v_readlane. fp16 weights convert exactly to fp16
+// pairs (each byte under exponent byte 0x64 is 1024 + b + 128; minus 1152) and
+// accumulate in fp32 with v_dot2_f32_f16; bf16 takes one conversion and one
+// FMA per weight. Per-channel scales only (applied to the reduced sum).
+// FLOOR: the measurement twin: the same grid, loads and chain, every loaded
+// word folded into a register instead of the math, no output.
+#ifndef SD_W8_CYC_WGS_PER_CU
+#define SD_W8_CYC_WGS_PER_CU 3
+#endif
+constexpr int kCycWgsPerCu = SD_W8_CYC_WGS_PER_CU;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                          0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// a[0..3] per lane -> every lane of 16-lane row r holds the wave's sum of a[r]
+__device__ __forceinline__ float reduce4_rows(float a0, float a1, float a2, float a3) {
+  // lanes 0-31 of a0 meet lanes 32-63 of a0 (and a2's halves the other way)
+  auto x = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a0),
+                                            __builtin_bit_cast(uint32_t, a2), false, false);
+  auto y = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a1),
+                                            __builtin_bit_cast(uint32_t, a3), false, false);
+  const float s02 = __builtin_bit_cast(float, static_cast<uint32_t>(x[0])) +
+                    __builtin_bit_cast(float, static_cast<uint32_t>(x[1]));  // a0 | a2
+  const float s13 = __builtin_bit_cast(float, static_cast<uint32_t>(y[0])) +
+                    __builtin_bit_cast(float, static_cast<uint32_t>(y[1]));  // a1 | a3
+  // odd 16-lane rows of s02 meet even rows of s13: rows a0, a1, a2, a3
+  auto z = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, s02),
+                                            __builtin_bit_cast(uint32_t, s13), false, false);
+  float v = __builtin_bit_cast(float, static_cast<uint32_t>(z[0])) +
+            __builtin_bit_cast(float, static_cast<uint32_t>(z[1]));
+  v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  return v;
+}
+
+// 4 int8 -> two exact fp16 pairs (bytes 0, 1 and 2, 3)
+__device__ __forceinline__ void int8x4_to_f16x2(uint32_t w, sd::f16x2& lo, sd::f16x2& hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  const sd::f16x2 off = {static_cast<_Float16>(1152.f), static_cast<_Float16>(1152.f)};
+  lo = __builtin_bit_cast(sd::f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - off;
+  hi = __builtin_bit_cast(sd::f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - off;
+}
+
+template <typename T, int C, int MODE, bool FLOOR = false>
+__global__ __launch_bounds__(kThreads) void w8a16_cyc_kernel(W8Params p) {
+#pragma clang fp contract(off)
+  constexpr int R = 4;  // rows per reduction
+  const int lane = threadIdx.x & 63;
+  const int nb = gridDim.x;  // a multiple of 8
+  const int blk = (blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3);
+  const int gw = blk * kWaves + (threadIdx.x >> 6);
+  const int W = nb * kWaves;
+  const int n = gw < p.N ? (p.N - gw + W - 1) / W : 0;  // rows gw + j W, j < n
+  if (n == 0) return;
+  typedef u32x4 Row[C];
+  auto load_row = [&](Row& b, int j, int z) {
+    const int8_t* src = p.w + static_cast<int64_t>(gw + static_cast<int64_t>(j) * W) * p.ws + z;
+#pragma unroll
+    for (int c = 0; c < C; ++c)  // lanes past K: a valid address, unused
+      b[c] = sd::load16_stream(src + min(c * 1024 + 16 * lane, p.K - 16));
+  };
+  Row buf[2];
+  load_row(buf[0], 0, 0);
+  load_row(buf[1], n > 1 ? 1 : 0, 0);
+
+  float xv[1][C][16];
+  row_activations<T, 1, C, MODE>(p, lane, gw == 0, xv);
+  uint32_t xp[C][8];  // fp16: the activations as exact pairs
+  if constexpr (!__is_same(T, __bf16)) {
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xp[c][i] = sd::pack2<T>(xv[0][c][2 * i], xv[0][c][2 * i + 1]);
+  }
+  auto dot = [&](const Row& b) -> float {
+    float a = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const uint32_t ww[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
+      if constexpr (__is_same(T, __bf16)) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          a = fmaf(static_cast<float>(static_cast<int8_t>(ww[i >> 2] >> (8 * (i & 3)))), xv[0][c][i], a);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sd::f16x2 lo, hi;
+          int8x4_to_f16x2(ww[i], lo, hi);
+          a = __builtin_amdgcn_fdot2(lo, __builtin_bit_cast(sd::f16x2, xp[c][2 * i]), a, false);
+          a = __builtin_amdgcn_fdot2(hi, __builtin_bit_cast(sd::f16x2, xp[c][2 * i + 1]), a, false);
+        }
+      }
+    }
+    return a;
+  };
+
+  // scale / bias bits of row gw + (j0 + lane) W, gathered per 64 rows
+  const bool s32 = p.scale_dtype == SD_F32;
+  uint32_t sg = 0, bg = 0;
+  auto scale_of = [&](uint32_t bits) -> float {
+    if (s32) return __uint_as_float(bits);
+    const uint16_t h = static_cast<uint16_t>(bits);
+    return p.scale_dtype == SD_BF16 ? sd::from_bits<__bf16>(h) : sd::from_bits<_Float16>(h);
+  };
+  u32x4 fold = {0u, 0u, 0u, 0u};
+  for (int j0 = 0; j0 < n; j0 += R) {
+    if ((j0 & 63) == 0) {
+      const int64_t row = gw + static_cast<int64_t>(min(j0 + lane, n - 1)) * W;
+      sg = s32 ? static_cast<const uint32_t*>(p.scale)[row] : static_cast<const uint16_t*>(p.scale)[row];
+      if (p.bias) bg = p.bias[row];
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      Row& slot = buf[r & 1];
+      Row cur;
+#pragma unroll
+      for (int c = 0; c < C; ++c) cur[c] = slot[c];
+      int z;  // 0 once row j0 + r has arrived: the next load waits for it
+      asm volatile("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(cur[C - 1].x));
+      load_row(slot, min(j0 + r + 2, n - 1), z);
+      if constexpr (FLOOR) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) fold ^= cur[c];
+        acc[r] = 0.f;
+      } else {
+        acc[r] = dot(cur);
+      }
+    }
+    if constexpr (FLOOR) {
+      fold.x ^= sg ^ (bg << 16);
+      continue;
+    }
+    const float v = reduce4_rows(acc[0], acc[1], acc[2], acc[3]);
+    const int r = lane >> 4, jb = j0 & 63;
+    const uint32_t sb0 = __builtin_amdgcn_readlane(sg, jb), sb1 = __builtin_amdgcn_readlane(sg, jb + 1),
+                   sb2 = __builtin_amdgcn_readlane(sg, jb + 2), sb3 = __builtin_amdgcn_readlane(sg, jb + 3);
+    float out = v * scale_of(r == 0 ? sb0 : (r == 1 ? sb1 : (r == 2 ? sb2 : sb3)));
+    if (p.bias) {
+      const uint32_t bb0 = __builtin_amdgcn_readlane(bg, jb), bb1 = __builtin_amdgcn_readlane(bg, jb + 1),
+                     bb2 = __builtin_amdgcn_readlane(bg, jb + 2), bb3 = __builtin_amdgcn_readlane(bg, jb + 3);
+      out = out + sd::from_bits<T>(static_cast<uint16_t>(r == 0 ? bb0 : (r == 1 ? bb1 : (r == 2 ? bb2 : bb3))));
+    }
+    const int j = j0 + r;
+    if ((lane & 15) == 0 && j < n)
+      p.y[gw + static_cast<int64_t>(j) * W] = sd::to_bits<T>(out);
+  }
+  if constexpr (FLOOR) {
+    // data-dependent and practically never true: the loads cannot be dropped
+    float xs = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xs += xv[0][c][i];
     const uint32_t f = fold.x ^ fold.y ^ fold.z ^ fold.w ^ __float_as_uint(xs);
     if (f == 0x9E3779B9u && lane == 0) p.y[0] = static_cast<uint16_t>(f);
   }
@@ -1141,8 +1311,10 @@ int launch_all(const W8Params& p, const W8Plan& pl, hipStream_t st) {
 // and a per-channel scale. Up to 32 MiB of weights (the decoder layers' linears,
 // where launch latency dominates) each wave owns a contiguous range of about 4
 // rows; the tiled kernel is faster from 4 rows up (qkv at M = 7: 4.6 vs 4.9 us
-// with 8 rows here). Past 32 MiB (the lm_head) one row takes the batch-cyclic
-// form (CYC): 26.6 us at 151936 x 1024 against 29.9 us on the tiled kernel.
+// with 8 rows here). Past 32 MiB (the lm_head) one row takes the row-cyclic
+// kernel (w8a16_cyc_kernel); its batch-cyclic predecessor (4-row batches, two
+// in flight, 16 waves per CU) took 26.6 - 29.7 us at 151936 x 1024 against
+// 29.9 us on the tiled kernel.
 // The rule is the same for the plain, SiLU and norm forms, so a fused call and
 // its two-launch form always run the same GEMV. Paired rows (gate_up with the
 // SiLU epilogue) take it up to 32 MiB only.
@@ -1159,16 +1331,14 @@ template <typename T, int MR, int C, int MODE, bool PAIR = false, bool FLOOR = f
 int launch_rows_c(const W8Params& p, hipStream_t st) {
   if constexpr (MR == 1 && !PAIR) {
     if (static_cast<int64_t>(p.N) * p.K > kRowsNarrowBytes) {
-      // batches of 4 rows dealt to 16 waves per CU in turn (lm_head at M = 1:
-      // 26.6 us; 8-row batches at 8 waves 26.9, 2-row batches at 32 waves 26.7,
-      // 16 waves of 8-row batches 29.5, same box)
-      constexpr int R = 4;
-      const int64_t batches = (static_cast<int64_t>(p.N) + R - 1) / R;
-      int64_t waves = static_cast<int64_t>(sd::device_cus()) * 16;
-      if (batches < waves) waves = batches;
-      const int blocks = static_cast<int>((waves + kWaves - 1) / kWaves);
-      hipLaunchKernelGGL((w8a16_rows_kernel<T, 1, C, R, MODE, false, true, FLOOR>), dim3(blocks),
-                         dim3(kThreads), 0, st, p, 0);
+      // row-cyclic (w8a16_cyc_kernel): a grid of a multiple of 8 workgroups
+      // (the XCD renumbering), kCycWgsPerCu per CU
+      int64_t blocks = static_cast<int64_t>(sd::device_cus()) * kCycWgsPerCu;
+      const int64_t need = (static_cast<int64_t>(p.N) + kWaves - 1) / kWaves;
+      if (blocks > need) blocks = need;
+      blocks = (blocks + 7) / 8 * 8;
+      hipLaunchKernelGGL((w8a16_cyc_kernel<T, C, MODE, FLOOR>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kThreads), 0, st, p);
       return SD_OK;
     }
   }
@@ -1185,18 +1355,18 @@ int launch_rows_c(const W8Params& p, hipStream_t st) {
     // 8 weight rows (4 pairs) per batch; 4 from three column chunks up, where
     // two batches of 8 rows fill the register file
     constexpr int RPAIR = C >= 3 ? 4 : 8;
-    hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, RPAIR, MODE, true, false, FLOOR>),
+    hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, RPAIR, MODE, true, FLOOR>),
                        dim3(blocks), dim3(kThreads), 0, st, p, rpw);
     return SD_OK;
   }
   if constexpr (MR == 1 && C == 1) {
     if (rpw >= 32) {
-      hipLaunchKernelGGL((w8a16_rows_kernel<T, 1, 1, 8, MODE, false, false, FLOOR>), dim3(blocks),
+      hipLaunchKernelGGL((w8a16_rows_kernel<T, 1, 1, 8, MODE, false, FLOOR>), dim3(blocks),
                          dim3(kThreads), 0, st, p, rpw);
       return SD_OK;
     }
   }
-  hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 4, MODE, false, false, FLOOR>), dim3(blocks),
+  hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 4, MODE, false, FLOOR>), dim3(blocks),
                      dim3(kThreads), 0, st, p, rpw);
   return SD_OK;
 }

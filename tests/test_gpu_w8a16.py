@@ -354,22 +354,29 @@ def test_gate_up_silu_entry_refuses_shapes_off_its_paths():
 # ------------------------------------------------- wide matrices at one row
 @pytest.mark.parametrize("N,K", [(151936, 1024), (16411, 2048), (32771, 1024), (8209, 4096)])
 @pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
-def test_batch_cyclic_rows_on_wide_matrices(N, K, act):
-    # one activation row on more than 32 MiB of weights takes the row kernel
-    # with batches of 4 rows dealt to the waves in turn: N not a multiple of
-    # the batch, of the waves, or of 16; 1 - 4 column chunks; bias
+@pytest.mark.parametrize("scale_f32", [False, True])
+def test_row_cyclic_rows_on_wide_matrices(N, K, act, scale_f32):
+    # one activation row on more than 32 MiB of weights takes the row-cyclic
+    # kernel (row n on wave n % W, four rows per lane reduction, scales gathered
+    # 64 rows at a time): N not a multiple of 4, of the waves, or of 64; 1 - 4
+    # column chunks; bias; 16-bit and fp32 scales
     assert N * K > 32 << 20
     c = workloads.w8a16_case(1, N, K, seed=N + K, act_dtype=act)
+    s = c["s"].float() if scale_f32 else c["s"]
     g = workloads.device_generator(DEV, N)
     bias = torch.randn((N,), generator=g, device=DEV).to(act)
-    y = ops.w8a16_linear(c["x"], c["w"], c["s"], bias)
-    check(y, c["x"], c["w"], c["s"], bias,
+    y = ops.w8a16_linear(c["x"], c["w"], s, bias)
+    check(y, c["x"], c["w"], s, bias,
           out_rel=2.0 ** -9 if act == torch.float16 else 2.0 ** -8, what=f"cyclic N={N} K={K}")
     # every output written exactly once: a second call into a NaN-filled
     # buffer gives the same bits
     out = torch.full_like(y, float("nan"))
-    ops.w8a16_linear(c["x"], c["w"], c["s"], bias, out=out)
+    ops.w8a16_linear(c["x"], c["w"], s, bias, out=out)
     assert torch.equal(out, y)
+    # without bias: the same sums less the bias, within the output rounding
+    y0 = ops.w8a16_linear(c["x"], c["w"], s)
+    check(y0, c["x"], c["w"], s, out_rel=2.0 ** -9 if act == torch.float16 else 2.0 ** -8,
+          what=f"cyclic N={N} K={K} no bias")
 
 
 def test_two_rows_on_wide_matrices_stay_on_the_tiled_kernel():
