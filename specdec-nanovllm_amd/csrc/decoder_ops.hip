@@ -30,22 +30,6 @@ constexpr int kThreads = 256;
 template <typename T> __device__ __forceinline__ float ld(const uint16_t* p, int64_t i) {
   return sd::from_bits<T>(p[i]);
 }
-template <typename T> __device__ __forceinline__ float round16(float x) {
-  return static_cast<float>(sd::round16<T>(x));
-}
-
-// Block-wide fp32 sum (every thread gets it). `red` holds kThreads / 64 floats.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) s += red[w];
-  return s;
-}
 
 // ------------------------------------------------------------------ RMSNorm
 // One workgroup per row; thread t holds 8-element chunks t, t + 256, ...
@@ -141,20 +125,9 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(RopeParams p) {
     }
     return;
   }
-  float x0 = ld<T>(x, lane), x1 = ld<T>(x, lane + 64);
-  if (w) {
-    float ss = x0 * x0 + x1 * x1;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    const float r = rsqrtf(ss / 128.f + p.eps);
-    x0 = round16<T>(round16<T>(x0 * r) * ld<T>(w, lane));
-    x1 = round16<T>(round16<T>(x1 * r) * ld<T>(w, lane + 64));
-  }
-  const float c = p.cos_sin[pos * p.cs_stride + lane];
-  const float s = p.cos_sin[pos * p.cs_stride + 64 + lane];
-  const float a = x0 * c, b = x1 * s;
-  const float e = x1 * c, f = x0 * s;
-  const uint16_t lo = sd::to_bits<T>(a - b), hi = sd::to_bits<T>(e + f);
+  uint16_t lo, hi;
+  sd::head_norm_rope<T>(ld<T>(x, lane), ld<T>(x, lane + 64), w, p.eps,
+                        p.cos_sin + pos * p.cs_stride, lo, hi);
   x[lane] = lo;
   x[lane + 64] = hi;
   if (kdst) {

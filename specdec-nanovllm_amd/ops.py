@@ -376,6 +376,11 @@ def w8a16_silu_linear(gate_up: torch.Tensor, qweight: torch.Tensor, scale: torch
     return y.view(*gate_up.shape[:-1], N)
 
 
+# Rows up to which the add + RMSNorm runs inside the projection's launch (the
+# fused entry points accept more; past this the two launches measured faster).
+NORM_FUSED_MAX_ROWS = 4
+
+
 def w8a16_rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
                          qweight: torch.Tensor, scale: torch.Tensor,
                          bias: torch.Tensor | None = None, group_size: int = 0,
@@ -425,7 +430,7 @@ def w8a16_rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     if M == 0:
         return y.view(shape)
     rc = _lib.SD_ERR_UNSUPPORTED
-    if M <= 4 and K % 8 == 0 and K <= 8192:
+    if M <= NORM_FUSED_MAX_ROWS and K % 8 == 0 and K <= 8192:
         lib = _lib.load()
         with torch.cuda.device(dev):
             rc = lib.sd_w8a16_rmsnorm_linear(
@@ -500,7 +505,7 @@ def w8a16_gate_up_silu(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tens
         return y.view(shape)
     lib = _lib.load()
     xa, ra, roa, nwa = x2, r2, ro, nw
-    if nw is not None and M > 4 and K % 8 == 0 and K <= 8192:
+    if nw is not None and M > NORM_FUSED_MAX_ROWS and K % 8 == 0 and K <= 8192:
         # the staged norm pays at up to 4 rows (every workgroup normalises all of
         # them): the RMSNorm launch (writing residual_out itself), then the
         # paired projection on the normalised rows
