@@ -186,14 +186,26 @@ def read_ceiling(ops, torch):
                     "groups; copy: torch copy_ of 512 MiB, read + write bytes"}
 
 
+def chain_len(steps, sets, cap=60):
+    """Steps per graph of the timed decode chain: ``steps`` itself when it is at
+    most ``cap``, else its largest divisor up to ``cap`` that is at least ``sets``
+    (so that exactly ``steps`` steps are whole replays), else ``sets``."""
+    if steps <= cap:
+        return max(steps, 1)
+    for n in range(cap, sets - 1, -1):
+        if steps % n == 0:
+            return n
+    return sets
+
+
 def time_steps(chain_graph, step_graphs, steps, warmup, torch):
     """ms per decode step over exactly ``steps`` steps: steps // n replays of
-    ``chain_graph`` (the n = len(step_graphs) steps back to back in one graph,
-    as a model forward holds every layer's attention call in one graph), then
-    the remainder as single-step graphs."""
-    n = len(step_graphs)
+    ``chain_graph`` (n consecutive steps in one graph, cycling over the page
+    sets, as a model forward holds every layer's attention call in one graph),
+    then any remainder as single-step graphs."""
+    n = chain_graph.steps
     settle(chain_graph, torch)  # untimed: the clocks settle (see settle)
-    for _ in range(max(1, warmup // n)):
+    for _ in range(max(1, -(-warmup // n))):
         chain_graph.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
@@ -202,7 +214,7 @@ def time_steps(chain_graph, step_graphs, steps, warmup, torch):
     for _ in range(steps // n):
         chain_graph.replay()
     for i in range(steps % n):
-        step_graphs[i].replay()
+        step_graphs[i % len(step_graphs)].replay()
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
@@ -811,7 +823,13 @@ def main():
         ops.paged_attention(q, kc, vc, tables[i], case["scale"], context_lens=lens_d, out=out,
                             twin="main", workspace=twin_ws[i])
     combine_graphs = [graph_of(chain(combine_fn), torch)]
-    step_chain = graph_of(chain(step_fn), torch)
+    # the timed chain: chain_len(steps) consecutive steps cycling over the page
+    # sets (each set's pages are cold again when it comes back: the other sets
+    # stream more than the MALL holds in between)
+    n_chain = chain_len(args.steps, sets)
+    step_fns = [step_fn(i % sets) for i in range(n_chain)]
+    step_chain = graph_of(lambda: [f() for f in step_fns], torch)
+    step_chain.steps = n_chain
 
     # ---- timed region: exactly `steps` decode steps (each a full fused store +
     #      attention over its own page set), `sets` of them per graph
@@ -842,9 +860,9 @@ def main():
         "config": {"workload": f"C2 decode step B={B}: store_kvcache + paged decode attention, "
                                "Qwen3-4B attention 32q/8kv/128, ctx U[512,4096], 256-token "
                                f"pages, 2048-page pool, {sets} disjoint page sets, one "
-                               f"step per set, {sets} consecutive steps per HIP graph",
+                               f"step per set in turn, {n_chain} consecutive steps per HIP graph",
                    "batch": B, "context_lens_sum": int(lens.sum()),
-                   "steps_per_graph": sets,
+                   "steps_per_graph": n_chain,
                    "algorithmic_bytes_per_step": step_bytes,
                    "frac_of_peak": round(value / PEAK_HBM_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,

@@ -923,10 +923,14 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
 // Four rows' sums reduce across the lanes with two lane-half swaps
 // (v_permlane32_swap, v_permlane16_swap) and four DPP adds, without LDS; the
 // scales (and bias) of a wave's next 64 rows are gathered once, one row per
-// lane, and read back with v_readlane. fp16 weights convert exactly to fp16
-// pairs (each byte under exponent byte 0x64 is 1024 + b + 128; minus 1152) and
-// accumulate in fp32 with v_dot2_f32_f16; bf16 takes one conversion and one
-// FMA per weight. Per-channel scales only (applied to the reduced sum).
+// lane, and read back with v_readlane. fp16: each weight byte b becomes the
+// exact fp16 value 1152 + b (b ^ 0x80 under exponent byte 0x64), the pairs
+// accumulate in fp32 with v_dot2_f32_f16, and 1152 times the lane's activation
+// sum comes off once per row (two instructions per 4 weights fewer than
+// subtracting 1152 from each; the products stay exact, the larger fp32 partial
+// sums add a rounding about 2^-8 of the 16-bit output's); bf16 takes one
+// conversion and one FMA per weight. Per-channel scales only (applied to the
+// reduced sum).
 // FLOOR: the measurement twin: the same grid, loads and chain, every loaded
 // word folded into a register instead of the math, no output.
 #ifndef SD_W8_CYC_WGS_PER_CU
@@ -963,12 +967,12 @@ __device__ __forceinline__ float reduce4_rows(float a0, float a1, float a2, floa
   return v;
 }
 
-// 4 int8 -> two exact fp16 pairs (bytes 0, 1 and 2, 3)
-__device__ __forceinline__ void int8x4_to_f16x2(uint32_t w, sd::f16x2& lo, sd::f16x2& hi) {
+// 4 int8 b -> two pairs of the exact fp16 values 1152 + b (bytes 0, 1 and 2, 3):
+// b ^ 0x80 under exponent byte 0x64 is 1024 + (b + 128)
+__device__ __forceinline__ void int8x4_to_biased_f16x2(uint32_t w, sd::f16x2& lo, sd::f16x2& hi) {
   const uint32_t u = w ^ 0x80808080u;
-  const sd::f16x2 off = {static_cast<_Float16>(1152.f), static_cast<_Float16>(1152.f)};
-  lo = __builtin_bit_cast(sd::f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - off;
-  hi = __builtin_bit_cast(sd::f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - off;
+  lo = __builtin_bit_cast(sd::f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
+  hi = __builtin_bit_cast(sd::f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
 }
 
 template <typename T, int C, int MODE, bool FLOOR = false>
@@ -978,16 +982,22 @@ __global__ __launch_bounds__(kThreads) void w8a16_cyc_kernel(W8Params p) {
   const int lane = threadIdx.x & 63;
   const int nb = gridDim.x;  // a multiple of 8
   const int blk = (blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3);
-  const int gw = blk * kWaves + (threadIdx.x >> 6);
+  // the wave index in an SGPR: row addresses are scalar (base + j x stride), so a
+  // row load is one instruction with a scalar base and the lane's offset
+  const int gw = blk * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = nb * kWaves;
   const int n = gw < p.N ? (p.N - gw + W - 1) / W : 0;  // rows gw + j W, j < n
   if (n == 0) return;
-  typedef u32x4 Row[C];
-  auto load_row = [&](Row& b, int j, int z) {
-    const int8_t* src = p.w + static_cast<int64_t>(gw + static_cast<int64_t>(j) * W) * p.ws + z;
+  const int8_t* const wbase = p.w + static_cast<int64_t>(gw) * p.ws;
+  const int64_t wstride = static_cast<int64_t>(W) * p.ws;  // bytes from row j to j + 1
+  uint32_t koff[C];  // lanes past K: a valid offset, unused
 #pragma unroll
-    for (int c = 0; c < C; ++c)  // lanes past K: a valid address, unused
-      b[c] = sd::load16_stream(src + min(c * 1024 + 16 * lane, p.K - 16));
+  for (int c = 0; c < C; ++c) koff[c] = static_cast<uint32_t>(min(c * 1024 + 16 * lane, p.K - 16));
+  typedef u32x4 Row[C];
+  auto load_row = [&](Row& b, int j, uint32_t z) {
+    const int8_t* src = wbase + j * wstride;
+#pragma unroll
+    for (int c = 0; c < C; ++c) b[c] = sd::load16_stream(src + (koff[c] + z));
   };
   Row buf[2];
   load_row(buf[0], 0, 0);
@@ -995,12 +1005,22 @@ __global__ __launch_bounds__(kThreads) void w8a16_cyc_kernel(W8Params p) {
 
   float xv[1][C][16];
   row_activations<T, 1, C, MODE>(p, lane, gw == 0, xv);
-  uint32_t xp[C][8];  // fp16: the activations as exact pairs
+  // fp16: the activations as exact pairs, and 1152 times their sum (this lane's
+  // columns): each weight byte enters the dot products as the exact fp16 value
+  // 1152 + b, and the 1152 x sum is taken off once per row
+  uint32_t xp[C][8];
+  float xoff = 0.f;
   if constexpr (!__is_same(T, __bf16)) {
 #pragma unroll
     for (int c = 0; c < C; ++c)
 #pragma unroll
       for (int i = 0; i < 8; ++i) xp[c][i] = sd::pack2<T>(xv[0][c][2 * i], xv[0][c][2 * i + 1]);
+    float xs = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xs += xv[0][c][i];
+    xoff = 1152.f * xs;
   }
   auto dot = [&](const Row& b) -> float {
     float a = 0.f;
@@ -1015,12 +1035,13 @@ __global__ __launch_bounds__(kThreads) void w8a16_cyc_kernel(W8Params p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           sd::f16x2 lo, hi;
-          int8x4_to_f16x2(ww[i], lo, hi);
+          int8x4_to_biased_f16x2(ww[i], lo, hi);
           a = __builtin_amdgcn_fdot2(lo, __builtin_bit_cast(sd::f16x2, xp[c][2 * i]), a, false);
           a = __builtin_amdgcn_fdot2(hi, __builtin_bit_cast(sd::f16x2, xp[c][2 * i + 1]), a, false);
         }
       }
     }
+    if constexpr (!__is_same(T, __bf16)) a = a - xoff;
     return a;
   };
 
@@ -1046,7 +1067,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_cyc_kernel(W8Params p) {
       Row cur;
 #pragma unroll
       for (int c = 0; c < C; ++c) cur[c] = slot[c];
-      int z;  // 0 once row j0 + r has arrived: the next load waits for it
+      uint32_t z;  // 0 once row j0 + r has arrived: the next load waits for it
       asm volatile("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(cur[C - 1].x));
       load_row(slot, min(j0 + r + 2, n - 1), z);
       if constexpr (FLOOR) {
