@@ -228,7 +228,7 @@ struct LaneSeq {
 template <bool STORE>
 __device__ __forceinline__ LaneSeq lane_seq(const AttnParams& p) {
   const int lane = threadIdx.x & 63;
-  LaneSeq ls;
+  LaneSeq ls{};
   ls.L = 0;
   ls.nq = 1;
   ls.q0 = lane;
@@ -254,15 +254,14 @@ __device__ __forceinline__ LaneSeq lane_seq(const AttnParams& p) {
   return ls;
 }
 
-// SeqInfo of sequence `src` (wave-uniform) from a lane_seq pass; the fields
-// are wave-uniform, so they are moved to scalar registers (control flow on
-// them stays uniform).
+// SeqInfo of sequence `src` (wave-uniform) from a lane_seq pass, read with
+// v_readlane into scalar registers (control flow on them stays uniform).
 __device__ __forceinline__ SeqInfo seq_info_of(const AttnParams& p, const LaneSeq& ls, int src) {
   SeqInfo si;
-  si.L = __builtin_amdgcn_readfirstlane(__shfl(ls.walk, src));
-  si.nq = __builtin_amdgcn_readfirstlane(__shfl(ls.nq, src));
-  si.q0 = __builtin_amdgcn_readfirstlane(__shfl(ls.q0, src));
-  si.causal = __builtin_amdgcn_readfirstlane(__shfl(ls.L, src)) - si.nq;
+  si.L = __builtin_amdgcn_readlane(ls.walk, src);
+  si.nq = __builtin_amdgcn_readlane(ls.nq, src);
+  si.q0 = __builtin_amdgcn_readlane(ls.q0, src);
+  si.causal = __builtin_amdgcn_readlane(ls.L, src) - si.nq;
   si.R = p.G * si.nq;
   return si;
 }
@@ -272,10 +271,11 @@ __device__ __forceinline__ SeqInfo seq_info_of(const AttnParams& p, const LaneSe
 // SeqInfo. False when the run has no columns.
 template <bool STORE>
 __device__ __forceinline__ bool run_start(const AttnParams& p, int run, int& total, int& S,
-                                          int& s0, int& b, int& first, SeqInfo& si) {
+                                          int& s0, int& b, int& first, SeqInfo& si,
+                                          LaneSeq& ls) {
   if (p.num_seqs <= 64) {
     const int lane = threadIdx.x & 63;
-    const LaneSeq ls = lane_seq<STORE>(p);
+    ls = lane_seq<STORE>(p);
     total = __builtin_amdgcn_readfirstlane(__shfl(ls.incl, 63));
     S = max((total + p.runs - 1) / p.runs, p.min_steps);
     s0 = run * S;
@@ -434,7 +434,11 @@ void paged_attn_main(AttnParams p) {
   const int run = static_cast<int>(blockIdx.x) / groups;
   int total, S, s0, b, first;
   SeqInfo si;
-  if (!run_start<STORE>(p, run, total, S, s0, b, first, si)) return;
+  // up to 64 sequences: every sequence's lengths stay in the lanes of `ls`, so a
+  // pair switch reads the next sequence's info from registers, not memory
+  LaneSeq ls{};
+  if (!run_start<STORE>(p, run, total, S, s0, b, first, si, ls)) return;
+  const bool lane_seqs = p.num_seqs <= 64;
   const int s1 = min(s0 + S, total);
   b = __builtin_amdgcn_readfirstlane(b);
   first = __builtin_amdgcn_readfirstlane(first);
@@ -763,7 +767,7 @@ void paged_attn_main(AttnParams p) {
       nj = 0;
       do {
         ++nb;
-        nL = walk_keys_uniform<STORE>(p, nb);
+        nL = lane_seqs ? __builtin_amdgcn_readlane(ls.walk, nb) : walk_keys_uniform<STORE>(p, nb);
       } while (nL == 0);  // sequences without keys own no columns; s + 1 < total ends the scan
     }
     // the last step issues a dummy prefetch so that every iteration issues the
@@ -776,7 +780,7 @@ void paged_attn_main(AttnParams p) {
     if (!more) return false;
     if (nb != b) {
       b = nb;
-      si = seq_info<STORE>(p, b);
+      si = lane_seqs ? seq_info_of(p, ls, b) : seq_info<STORE>(p, b);
       n = steps_of(p, si.L);
       j_first = 0;
       begin_pair();
