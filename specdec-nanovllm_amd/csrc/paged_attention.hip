@@ -192,21 +192,16 @@ __device__ void locate(const AttnParams& p, int s, int& b_out, int& first_out) {
   for (int c = 0; c < p.num_seqs; c += 64) {
     const int b = c + lane;
     const int n = b < p.num_seqs ? steps_of(p, walk_keys<STORE>(p, b)) : 0;
-    int incl = n;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off);
-      if (lane >= off) incl += t;
-    }
+    const int incl = sd::wave_inclusive_sum(n);
     const int excl = run + incl - n;
     const unsigned long long hit = __ballot(n > 0 && excl <= s && s < excl + n);
     if (hit) {
       const int src = __ffsll(static_cast<unsigned long long>(hit)) - 1;
       b_out = c + src;
-      first_out = __shfl(excl, src);
+      first_out = __builtin_amdgcn_readlane(excl, src);
       return;
     }
-    run += __shfl(incl, 63);
+    run += __builtin_amdgcn_readlane(incl, 63);
   }
   b_out = p.num_seqs - 1;  // s >= total: callers never ask
   first_out = run;
@@ -229,28 +224,26 @@ template <bool STORE>
 __device__ __forceinline__ LaneSeq lane_seq(const AttnParams& p) {
   const int lane = threadIdx.x & 63;
   LaneSeq ls{};
-  ls.L = 0;
-  ls.nq = 1;
-  ls.q0 = lane;
   const bool in = lane < p.num_seqs;
-  if (in) {
-    const int L = p.ctx ? p.ctx[lane] : (p.cu_k[lane + 1] - p.cu_k[lane]);
-    ls.L = min(max(L, 0), p.max_ctx);
-    if (p.cu_q) {
-      const int a = p.cu_q[lane], c = p.cu_q[lane + 1];
-      ls.q0 = a;
-      ls.nq = min(max(c - a, 0), p.max_qlen);
-    }
-  }
+  // Every load first, then the arithmetic: the arrays are picked with uniform
+  // selects and the index clamped (lanes past num_seqs read the last
+  // sequence's words, never used). Loads under the branches on ctx / cu_q made
+  // the compiler wait for the key lengths before it issued the query offsets'
+  // loads, two round trips.
+  const int li = min(lane, p.num_seqs - 1);  // num_seqs >= 1 on every launch
+  const int32_t* kp = p.ctx ? p.ctx : p.cu_k;
+  const int32_t* qp = p.cu_q ? p.cu_q : kp;
+  const int nx = p.ctx ? 0 : 1;  // cu_k: the next offset
+  const int nqx = p.cu_q ? 1 : 0;
+  const int k0 = kp[li], k1 = kp[li + nx];
+  const int q0 = qp[li], q1 = qp[li + nqx];
+  const int L = p.ctx ? k0 : k1 - k0;
+  ls.L = in ? min(max(L, 0), p.max_ctx) : 0;
+  ls.q0 = p.cu_q && in ? q0 : lane;
+  ls.nq = p.cu_q ? (in ? min(max(q1 - q0, 0), p.max_qlen) : 1) : 1;
   ls.walk = STORE ? max(ls.L - ls.nq, 0) : ls.L;
   ls.n = in ? steps_of(p, ls.walk) : 0;
-  int incl = ls.n;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(incl, off);
-    if (lane >= off) incl += t;
-  }
-  ls.incl = incl;
+  ls.incl = sd::wave_inclusive_sum(ls.n);
   return ls;
 }
 
@@ -276,14 +269,14 @@ __device__ __forceinline__ bool run_start(const AttnParams& p, int run, int& tot
   if (p.num_seqs <= 64) {
     const int lane = threadIdx.x & 63;
     ls = lane_seq<STORE>(p);
-    total = __builtin_amdgcn_readfirstlane(__shfl(ls.incl, 63));
+    total = __builtin_amdgcn_readlane(ls.incl, 63);
     S = max((total + p.runs - 1) / p.runs, p.min_steps);
     s0 = run * S;
     if (s0 >= total) return false;
     const int excl = ls.incl - ls.n;
     const unsigned long long hit = __ballot(ls.n > 0 && excl <= s0 && s0 < ls.incl);
     b = __ffsll(static_cast<unsigned long long>(hit)) - 1;
-    first = __shfl(excl, b);
+    first = __builtin_amdgcn_readlane(excl, b);
     si = seq_info_of(p, ls, b);
     (void)lane;
     return true;
@@ -302,10 +295,11 @@ __device__ __forceinline__ bool run_start(const AttnParams& p, int run, int& tot
 // slots bit for bit (slot -1 or outside the pool: skipped), as store_kvcache
 // does. The main kernel reads only cached keys, so the combine kernel, which
 // runs after it, does the copies: each thread loads its first piece on entry
-// and writes it after its merge.
+// and writes it after its merge. The slot stays the raw 32-bit value until the
+// write: widening it where it is loaded would wait for the load right there.
 struct StorePiece {
   u32x4 data;
-  int64_t slot;
+  int32_t slot;
   int64_t tok;
   int head;
   int piece;
@@ -332,8 +326,9 @@ __device__ __forceinline__ void load_piece(const AttnParams& p, StorePiece& sp) 
 }
 
 __device__ __forceinline__ void write_piece(const AttnParams& p, const StorePiece& sp) {
-  if (sp.slot < 0 || sp.slot >= p.num_slots) return;
-  const int64_t blk = sp.slot / p.block_size, off = sp.slot - blk * p.block_size;
+  const int64_t slot = sp.slot;
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int64_t blk = slot / p.block_size, off = slot - blk * p.block_size;
   uint16_t* dst = const_cast<uint16_t*>(sp.is_v ? p.vc : p.kc) + blk * p.c_sblk +
                   off * p.c_spos + sp.head * p.c_shead;
   sd::store16(dst + sp.piece * 8, sp.data);
@@ -800,12 +795,20 @@ void paged_attn_main(AttnParams p) {
   }
 }
 
-// Four consecutive 16-bit elements as fp32.
+// Four consecutive 16-bit elements: their bits, and as fp32.
+__device__ __forceinline__ uint2 load_bits4(const uint16_t* src) {
+  return *reinterpret_cast<const uint2*>(src);
+}
+
 template <typename T>
-__device__ __forceinline__ f32x4 load4f(const uint16_t* src) {
-  const uint2 w = *reinterpret_cast<const uint2*>(src);
+__device__ __forceinline__ f32x4 to4f(uint2 w) {
   return f32x4{sd::from_bits<T>(static_cast<uint16_t>(w.x)), sd::from_bits<T>(static_cast<uint16_t>(w.x >> 16)),
                sd::from_bits<T>(static_cast<uint16_t>(w.y)), sd::from_bits<T>(static_cast<uint16_t>(w.y >> 16))};
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4 load4f(const uint16_t* src) {
+  return to4f<T>(load_bits4(src));
 }
 
 // Wave-wide: the columns of sequences [0, b) and of all sequences, one pass.
@@ -846,12 +849,12 @@ __device__ void cols_split(const AttnParams& p, int b, int& before, int& total) 
 // new keys (new row j at position L - n_b + j, seen by query rows qi >= j) are
 // merged last: s_j = q . k_j from the 16-bit inputs in fp32, k_j / v_j from
 // key / value — or from the cache row when the row's slot is not stored (-1
-// or outside the pool), as an unfused store would leave it. Their loads are
-// issued first, beside the scan of the lengths.
-template <typename T, bool STORE>
+// or outside the pool), as an unfused store would leave it. The first NK new
+// rows' loads go out with the partials' (the rest, rows NK.., one at a time at
+// the end; NK = 1 for decode).
+template <typename T, bool STORE, int NK = 8>
 __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   constexpr int kBatch = 16;   // partial loads in flight per thread
-  constexpr int kNewMax = 8;   // new rows whose loads are issued up front
   constexpr int kGroups = kCombThreads / 32;
   __shared__ __attribute__((aligned(16))) float4 s_o[kGroups][32];
   __shared__ float2 s_ml[kGroups];
@@ -862,8 +865,8 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   if (p.num_seqs <= 64) {
     const LaneSeq ls = lane_seq<STORE>(p);
     si = seq_info_of(p, ls, b);
-    total = __shfl(ls.incl, 63);
-    f = __shfl(ls.incl - ls.n, b);
+    total = __builtin_amdgcn_readlane(ls.incl, 63);
+    f = __builtin_amdgcn_readlane(ls.incl - ls.n, b);
   } else {
     si = seq_info<STORE>(p, b);
     cols_split<STORE>(p, b, f, total);
@@ -877,21 +880,24 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   const bool live = row < si.R && qt >= 0 && qt < p.total_q;
   const int n = steps_of(p, si.L);
 
-  // STORE: the new rows' key / value / slot and this row's q, loaded now
-  f32x4 qv = {0.f, 0.f, 0.f, 0.f}, kn[kNewMax] = {}, vn[kNewMax] = {};
-  int64_t sn[kNewMax] = {};
+  // STORE: this row's q and the first NK new rows' key / value / slot, loaded
+  // now, before the partials. The loads are unconditional, with every index
+  // clamped into range, and stay raw bits until they are used: under a per-row
+  // branch the compiler waited for each one before the branch joined (one round
+  // trip per new row).
+  uint2 qb = {0u, 0u}, kb[NK], vb[NK];
+  int32_t sn[NK];
   if constexpr (STORE) {
-    if (live && sl == 0) {
-      qv = load4f<T>(p.q + qt * p.q_stok + static_cast<int64_t>(h * p.G + g) * p.q_shead + d4);
+    const int64_t last_q = static_cast<int64_t>(p.total_q) - 1;
+    const int64_t qtc = min(max(qt, static_cast<int64_t>(0)), last_q);
+    qb = load_bits4(p.q + qtc * p.q_stok + static_cast<int64_t>(h * p.G + g) * p.q_shead + d4);
+    const int jl = max(si.nq - 1, 0);
 #pragma unroll
-      for (int j = 0; j < kNewMax; ++j) {
-        if (j < si.nq && j <= qi) {
-          const int64_t tr = si.q0 + j;
-          sn[j] = p.slot[tr];
-          kn[j] = load4f<T>(p.knew + tr * p.kn_stok + static_cast<int64_t>(h) * p.kn_shead + d4);
-          vn[j] = load4f<T>(p.vnew + tr * p.vn_stok + static_cast<int64_t>(h) * p.vn_shead + d4);
-        }
-      }
+    for (int j = 0; j < NK; ++j) {
+      const int64_t tr = min(max(si.q0 + min(j, jl), static_cast<int64_t>(0)), last_q);
+      sn[j] = p.slot[tr];
+      kb[j] = load_bits4(p.knew + tr * p.kn_stok + static_cast<int64_t>(h) * p.kn_shead + d4);
+      vb[j] = load_bits4(p.vnew + tr * p.vn_stok + static_cast<int64_t>(h) * p.vn_shead + d4);
     }
   }
 
@@ -909,37 +915,48 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
       const float2* ml = reinterpret_cast<const float2*>(p.ws_ml);
       const int64_t base = ((static_cast<int64_t>(w0) + b) * p.Hkv + h) * p.rmax + row;
       const int64_t run_stride = static_cast<int64_t>(p.Hkv) * p.rmax;  // rows between runs
-      for (int c0 = u0; c0 < u1; c0 += kBatch) {
+      // one batch: its loads all in flight, then the merge of those that exist.
+      // Entries past the slice's count load a partial of the pair again (the
+      // last one; never merged): a load under a branch whose other side writes
+      // a default into the same registers made the compiler wait for it, and
+      // for every load issued before it, at the branch.
+      auto merge_batch = [&](int c0) {
         float2 part[kBatch];
         f32x4 a[kBatch];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
-          const int64_t e = base + static_cast<int64_t>(c0 + u) * run_stride;
-          if (c0 + u < u1) {
-            part[u] = ml[e];
-            a[u] = __builtin_bit_cast(f32x4, sd::load16_stream(p.ws_acc + e * kD + d4));
-          } else {
-            part[u] = make_float2(-INFINITY, 0.f);
-            a[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-          }
+          const int cu = max(min(c0 + u, u1 - 1), 0);  // u1 >= 1 here (cnt >= 1)
+          const int64_t e = base + static_cast<int64_t>(cu) * run_stride;
+          part[u] = ml[e];
+          a[u] = __builtin_bit_cast(f32x4, sd::load16_stream(p.ws_acc + e * kD + d4));
         }
+        // all of the batch's loads before any use (left alone, the scheduler
+        // interleaved them with the merge and waited after every pair)
+        __builtin_amdgcn_sched_barrier(0);
         float mc = M;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) mc = fmaxf(mc, part[u].x);  // -inf past the count
-        if (mc == -INFINITY) continue;
-        const float r = sd::fast_exp2(M - mc);  // rescale what earlier batches summed
+        for (int u = 0; u < kBatch; ++u) mc = fmaxf(mc, c0 + u < u1 ? part[u].x : -INFINITY);
+        // No branch between the loads and their use (the compiler sinks loads
+        // past one, a second round trip): entries past the count get weight 0,
+        // and with no partial at all (mc = -inf, l = o = 0) the reference point
+        // 0 keeps every weight 0 instead of NaN.
+        const float mr = mc == -INFINITY ? 0.f : mc;
+        const float r = sd::fast_exp2(M - mr);  // rescale what earlier batches summed
         l *= r;
         o *= r;
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
-          if (c0 + u < u1) {  // false on the whole wave past the slice's count: skipped
-            const float w = sd::fast_exp2(part[u].x - mc);
-            l += w * part[u].y;
-            o += w * a[u];
-          }
+          const float w = c0 + u < u1 ? sd::fast_exp2(part[u].x - mr) : 0.f;
+          l += w * part[u].y;
+          o += w * a[u];
         }
         M = mc;
-      }
+      };
+      // The first batch stays out of the loop: the compiler waits for every load
+      // in flight before entering a loop whose body loads, which would put the
+      // STORE form's new-row loads a round trip ahead of the partials'.
+      merge_batch(u0);
+      for (int c0 = u0 + kBatch; c0 < u1; c0 += kBatch) merge_batch(c0);
     }
   }
   if (nsl > 1) {  // workgroup-uniform
@@ -972,6 +989,7 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   }
   if constexpr (STORE) {
     // the 32 lanes of this row hold 4 dims each; the dot products reduce over them
+    const f32x4 qv = to4f<T>(qb);
     const int L = seq_keys(p, b);
     const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
     auto merge_new = [&](int j, f32x4 kv, f32x4 vv, int64_t slot) {
@@ -991,16 +1009,19 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
       M = mn;
     };
     if (si.nq == 1) {  // decode: one new key (uniform over the row's lanes)
-      if (L - 1 >= 0) merge_new(0, kn[0], vn[0], sn[0]);
+      if (L - 1 >= 0) merge_new(0, to4f<T>(kb[0]), to4f<T>(vb[0]), sn[0]);
     } else {
       // several new keys: their unstored cache rows and their dot products first,
       // the butterflies of all keys interleaved (each a chain of five dependent
       // exchanges), then the merges in key order (the same operations in the
       // same order as one key at a time)
-      bool use[kNewMax];
-      float dot[kNewMax];
+      bool use[NK];
+      float dot[NK];
+      f32x4 kn[NK], vn[NK];
 #pragma unroll
-      for (int j = 0; j < kNewMax; ++j) {  // uniform over the row's lanes
+      for (int j = 0; j < NK; ++j) {  // uniform over the row's lanes
+        kn[j] = to4f<T>(kb[j]);
+        vn[j] = to4f<T>(vb[j]);
         use[j] = j < si.nq && j <= qi && L - si.nq + j >= 0;
         if (use[j] && !(sn[j] >= 0 && sn[j] < p.num_slots)) {  // not stored: the cache row stays
           const int64_t crow = kv_row(p, btrow, L - si.nq + j) + static_cast<int64_t>(h) * p.c_shead;
@@ -1009,14 +1030,14 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
         }
       }
 #pragma unroll
-      for (int j = 0; j < kNewMax; ++j)
+      for (int j = 0; j < NK; ++j)
         dot[j] = use[j] ? qv.x * kn[j].x + qv.y * kn[j].y + qv.z * kn[j].z + qv.w * kn[j].w : 0.f;
 #pragma unroll
       for (int off = 1; off < 32; off <<= 1)
 #pragma unroll
-        for (int j = 0; j < kNewMax; ++j) dot[j] += __shfl_xor(dot[j], off);
+        for (int j = 0; j < NK; ++j) dot[j] += __shfl_xor(dot[j], off);
 #pragma unroll
-      for (int j = 0; j < kNewMax; ++j) {
+      for (int j = 0; j < NK; ++j) {
         if (!use[j]) continue;
         const float sj = dot[j] * p.scale_log2;
         const float mn = fmaxf(M, sj);
@@ -1026,7 +1047,7 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
         M = mn;
       }
     }
-    for (int j = kNewMax; j < si.nq; ++j) {
+    for (int j = NK; j < si.nq; ++j) {
       if (L - si.nq + j < 0 || j > qi) continue;
       const int64_t tr = si.q0 + j;
       merge_new(j,
@@ -1038,8 +1059,11 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
   store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);
 }
 
-// STORE: the launch's share of the fused store (grid-stride over the pieces).
-template <typename T, bool STORE>
+// STORE: the launch's share of the fused store (grid-stride over the pieces;
+// the host launches nothing when total_q == 0, so items > 0). Every thread
+// loads a piece on entry, threads past the pieces the last one again (one
+// cache line), so no branch holds the load.
+template <typename T, bool STORE, int NK = 8>
 __global__ __launch_bounds__(kCombThreads) void paged_attn_combine(AttnParams p) {
   if constexpr (!STORE) {
     combine_rows<T, false>(p);
@@ -1049,11 +1073,9 @@ __global__ __launch_bounds__(kCombThreads) void paged_attn_combine(AttnParams p)
     const uint32_t it0 =
         ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
     StorePiece sp;
-    if (it0 < items) {
-      piece_of(p, it0, sp);
-      load_piece(p, sp);
-    }
-    combine_rows<T, true>(p);
+    piece_of(p, min(it0, items - 1), sp);
+    load_piece(p, sp);
+    combine_rows<T, true, NK>(p);
     if (it0 < items) write_piece(p, sp);
     for (uint32_t it = it0 + nthreads; it < items; it += nthreads) {
       piece_of(p, it, sp);
@@ -1120,7 +1142,9 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   // the row keeps one slice and the workgroup shrinks, with no LDS merge (C2
   // B = 32 combine 4.4 -> 4.1 us; more slices than 8 groups allow measured
   // slower for one sequence and for verify).
-  pl.comb_rows = 1;
+  // At least two rows (64 threads, a whole wave; a second row past rmax idles):
+  // the length scan runs on all 64 lanes of a wave, one sequence per lane.
+  pl.comb_rows = 2;
   while (pl.comb_rows < 8 && pl.comb_rows < pl.rmax) pl.comb_rows *= 2;
   const int64_t ns = num_seqs;
   const int64_t est = (3 * runs + 2 * ns - 1) / (2 * ns) + 2;
@@ -1183,7 +1207,9 @@ int launch_all(const AttnParams& p, const Plan& pl, RunMode mode, hipStream_t st
   }
   const dim3 grid((pl.rmax + p.comb_rows - 1) / p.comb_rows, p.Hkv, p.num_seqs);
   const dim3 block(static_cast<unsigned>(p.comb_rows * p.comb_slices * 32));
-  if (p.knew)
+  if (p.knew && p.max_qlen == 1)  // decode: one new row per sequence
+    hipLaunchKernelGGL((paged_attn_combine<T, true, 1>), grid, block, 0, st, p);
+  else if (p.knew)
     hipLaunchKernelGGL((paged_attn_combine<T, true>), grid, block, 0, st, p);
   else
     hipLaunchKernelGGL((paged_attn_combine<T, false>), grid, block, 0, st, p);

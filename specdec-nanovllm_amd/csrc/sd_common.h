@@ -167,6 +167,21 @@ __device__ __forceinline__ float sum_over_groups(float v) {
   return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves (VALU
+// latency, no LDS round trips): Hillis-Steele shifts by 1, 2, 4 and 8 inside
+// each row of 16 lanes (lanes whose source is outside the row add 0), then lane
+// 15's total added to row 1 and row 3 (row_bcast:15), then lane 31's total to
+// rows 2 and 3 (row_bcast:31). Every lane must be active.
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return x;
+}
+
 // 2^x on the transcendental unit (v_exp_f32) without denormal fix-ups:
 // results below 2^-126 flush to 0, 2^-inf = 0. Softmax weights only.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -170,6 +170,26 @@ def test_gqa_ratios(hq, hkv):
                       what=f"hq={hq} hkv={hkv}")
 
 
+@pytest.mark.parametrize("batch", [33, 40, 64])
+def test_mha_decode_between_33_and_64_sequences(batch):
+    # one query row per kv head (G = 1): the merge kernel's workgroup is one whole
+    # wave, whose 64 lanes each scan one sequence's length; plain and fused store
+    rng = np.random.default_rng(batch)
+    keys = rng.integers(1, 600, size=batch).tolist()
+    q, kc, vc, bt, lens = random_case(keys, hq=8, hkv=8, seed=900 + batch)
+    out = run_decode(q, kc, vc, bt, lens)
+    assert_close_attn(to_np(out), oracle(q, kc, vc, bt, lens, 128 ** -0.5),
+                      what=f"MHA decode B={batch}")
+    dg = workloads.device_generator(DEV, 950 + batch)
+    knew = torch.randn((batch, 8, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    vnew = torch.randn((batch, 8, 128), generator=dg, device=DEV).to(torch.bfloat16)
+    slots = workloads.slots_for(bt, [[L - 1] for L in keys], 256).to(DEV)
+    o, kc2, vc2 = _fused_vs_separate(q, kc, vc, bt.to(DEV), knew, vnew, slots, 128 ** -0.5,
+                                     context_lens=lens.to(DEV))
+    assert_close_attn(to_np(o), oracle(q, kc2, vc2, bt, lens, 128 ** -0.5),
+                      what=f"MHA fused decode B={batch}")
+
+
 def test_fp16():
     q, kc, vc, bt, lens = random_case([1234, 4000], dtype=torch.float16, seed=41)
     out = run_decode(q, kc, vc, bt, lens)
