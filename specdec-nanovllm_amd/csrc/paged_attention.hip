@@ -903,60 +903,119 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
 
   float M = -INFINITY, l = 0.f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  bool final_by_main = !STORE && n == 0;  // (zeros written below)
-  if (live && n > 0) {
-    const int S = max((total + p.runs - 1) / p.runs, p.min_steps);
-    const int w0 = f / S, w1 = (f + n - 1) / S;
-    if (!STORE && w0 == w1) final_by_main = true;
-    if (!final_by_main) {
-      const int cnt = w1 - w0 + 1;
-      const int per = (cnt + nsl - 1) / nsl;
-      const int u0 = sl * per, u1 = min(u0 + per, cnt);
-      const float2* ml = reinterpret_cast<const float2*>(p.ws_ml);
-      const int64_t base = ((static_cast<int64_t>(w0) + b) * p.Hkv + h) * p.rmax + row;
-      const int64_t run_stride = static_cast<int64_t>(p.Hkv) * p.rmax;  // rows between runs
-      // one batch: its loads all in flight, then the merge of those that exist.
-      // Entries past the slice's count load a partial of the pair again (the
-      // last one; never merged): a load under a branch whose other side writes
-      // a default into the same registers made the compiler wait for it, and
-      // for every load issued before it, at the branch.
-      auto merge_batch = [&](int c0) {
-        float2 part[kBatch];
-        f32x4 a[kBatch];
+  // Sequence b spans columns [f, f + n): runs w0 .. w1 met it (uniform over the
+  // workgroup). final_by_main: no keys, or (without STORE) one run, which wrote
+  // the output itself.
+  const int S = max((total + p.runs - 1) / p.runs, p.min_steps);
+  const int w0 = n > 0 ? f / S : 0, w1 = n > 0 ? (f + n - 1) / S : 0;
+  const bool final_by_main = !STORE && (n == 0 || w0 == w1);
+  const bool parts = n > 0 && !final_by_main;
+  const int cnt = w1 - w0 + 1;
+  const int per = (cnt + nsl - 1) / nsl;
+  const int u0 = sl * per, u1 = min(u0 + per, cnt);  // this slice's share; u1 >= 1
+  const float2* ml = reinterpret_cast<const float2*>(p.ws_ml);
+  // rows past the pair's (idle) read the last row of the slot
+  const int64_t base = ((static_cast<int64_t>(w0) + b) * p.Hkv + h) * p.rmax + min(row, p.rmax - 1);
+  const int64_t run_stride = static_cast<int64_t>(p.Hkv) * p.rmax;  // rows between runs
+  // One batch of partials: its loads all in flight, then the merge of those
+  // that exist. Entries past the slice's count load a partial of the pair again
+  // (the last one; never merged): a load under a branch whose other side writes
+  // a default into the same registers made the compiler wait for it, and for
+  // every load issued before it, at the branch.
+  float2 part[kBatch];
+  f32x4 a[kBatch];
+  auto load_batch = [&](int c0) {
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const int cu = max(min(c0 + u, u1 - 1), 0);  // u1 >= 1 here (cnt >= 1)
-          const int64_t e = base + static_cast<int64_t>(cu) * run_stride;
-          part[u] = ml[e];
-          a[u] = __builtin_bit_cast(f32x4, sd::load16_stream(p.ws_acc + e * kD + d4));
+    for (int u = 0; u < kBatch; ++u) {
+      const int cu = max(min(c0 + u, u1 - 1), 0);
+      const int64_t e = base + static_cast<int64_t>(cu) * run_stride;
+      part[u] = ml[e];
+      a[u] = __builtin_bit_cast(f32x4, sd::load16_stream(p.ws_acc + e * kD + d4));
+    }
+    // all of the batch's loads before any use (left alone, the scheduler
+    // interleaved them with the merge and waited after every pair)
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto merge_batch = [&](int c0) {
+    float mc = M;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) mc = fmaxf(mc, c0 + u < u1 ? part[u].x : -INFINITY);
+    // No branch between the loads and their use (the compiler sinks loads past
+    // one, a second round trip): entries past the count get weight 0, and with
+    // no partial at all (mc = -inf, l = o = 0) the reference point 0 keeps
+    // every weight 0 instead of NaN.
+    const float mr = mc == -INFINITY ? 0.f : mc;
+    const float r = sd::fast_exp2(M - mr);  // rescale what earlier batches summed
+    l *= r;
+    o *= r;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const float w = c0 + u < u1 ? sd::fast_exp2(part[u].x - mr) : 0.f;
+      l += w * part[u].y;
+      o += w * a[u];
+    }
+    M = mc;
+  };
+  // STORE: unconditional (the indices are valid without keys too): after a branch
+  // around them the compiler could not tell how many loads follow the new rows'
+  // and made the dot products below wait for the partials as well.
+  if (STORE || parts) load_batch(u0);
+
+  // STORE: while the partials are in flight, the new keys' rows and their dot
+  // products with q. The 32 lanes of a row hold 4 dims each and the products
+  // reduce over them (every lane of the wave takes part: no row has returned
+  // yet). A new row whose slot is not stored keeps the cache row, as an unfused
+  // store would leave it: one branch, taken only then. The merges come after the
+  // partials', in key order.
+  const int L = si.causal + si.nq;  // the sequence's keys, from the scan (no reload)
+  const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
+  auto merge_key = [&](float dot, const f32x4& vv) {
+    const float sj = dot * p.scale_log2;
+    const float mn = fmaxf(M, sj);
+    const float r = sd::fast_exp2(M - mn), w = sd::fast_exp2(sj - mn);
+    l = l * r + w;
+    o = o * r + w * vv;
+    M = mn;
+  };
+  // new row j is merged into this row when jlo <= j <= jhi (it exists, it is a
+  // key position, and the row sees it); bad: its slot is not stored
+  const int jhi = min(qi, si.nq - 1), jlo = si.nq - L;  // uniform over the row's lanes
+  const uint32_t ns32 =
+      static_cast<uint32_t>(p.num_slots < 0x80000000ll ? p.num_slots : 0x80000000ll);
+  float dot[NK];
+  if constexpr (STORE) {
+    uint32_t bad = 0;
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+      bad |= (static_cast<uint32_t>(sn[j]) >= ns32 && j >= jlo && j <= jhi) ? 1u << j : 0u;
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+      dot[j] = j >= jlo && j <= jhi ? sd::dot2<T>(qb.y, kb[j].y, sd::dot2<T>(qb.x, kb[j].x, 0.f)) : 0.f;
+    // Rows whose slot is not stored: the cache row's bits, and the product
+    // recomputed inside the branch. Loads in the branch that wrote registers read
+    // after it would make the compiler wait at the join for them, and so for
+    // every partial load issued before them.
+    if (bad) {
+#pragma unroll
+      for (int j = 0; j < NK; ++j) {
+        if (bad & (1u << j)) {
+          const int64_t crow = kv_row(p, btrow, L - si.nq + j) + static_cast<int64_t>(h) * p.c_shead;
+          const uint2 kc = load_bits4(p.kc + crow + d4);
+          vb[j] = load_bits4(p.vc + crow + d4);
+          dot[j] = sd::dot2<T>(qb.y, kc.y, sd::dot2<T>(qb.x, kc.x, 0.f));
+          asm volatile("" : "+v"(vb[j].x), "+v"(vb[j].y));  // vb[j] arrives here, not later
         }
-        // all of the batch's loads before any use (left alone, the scheduler
-        // interleaved them with the merge and waited after every pair)
-        __builtin_amdgcn_sched_barrier(0);
-        float mc = M;
+      }
+    }
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) mc = fmaxf(mc, c0 + u < u1 ? part[u].x : -INFINITY);
-        // No branch between the loads and their use (the compiler sinks loads
-        // past one, a second round trip): entries past the count get weight 0,
-        // and with no partial at all (mc = -inf, l = o = 0) the reference point
-        // 0 keeps every weight 0 instead of NaN.
-        const float mr = mc == -INFINITY ? 0.f : mc;
-        const float r = sd::fast_exp2(M - mr);  // rescale what earlier batches summed
-        l *= r;
-        o *= r;
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const float w = c0 + u < u1 ? sd::fast_exp2(part[u].x - mr) : 0.f;
-          l += w * part[u].y;
-          o += w * a[u];
-        }
-        M = mc;
-      };
-      // The first batch stays out of the loop: the compiler waits for every load
-      // in flight before entering a loop whose body loads, which would put the
-      // STORE form's new-row loads a round trip ahead of the partials'.
-      merge_batch(u0);
-      for (int c0 = u0 + kBatch; c0 < u1; c0 += kBatch) merge_batch(c0);
+    for (int j = 0; j < NK; ++j) dot[j] = sd::half_wave_sum(dot[j]);
+  }
+
+  if (parts) {
+    merge_batch(u0);
+    for (int c0 = u0 + kBatch; c0 < u1; c0 += kBatch) {
+      load_batch(c0);
+      merge_batch(c0);
     }
   }
   if (nsl > 1) {  // workgroup-uniform
@@ -988,72 +1047,24 @@ __device__ __forceinline__ void combine_rows(const AttnParams& p) {
     return;
   }
   if constexpr (STORE) {
-    // the 32 lanes of this row hold 4 dims each; the dot products reduce over them
-    const f32x4 qv = to4f<T>(qb);
-    const int L = seq_keys(p, b);
-    const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
-    auto merge_new = [&](int j, f32x4 kv, f32x4 vv, int64_t slot) {
-      if (!(slot >= 0 && slot < p.num_slots)) {  // not stored: the cache row stays
-        const int64_t crow = kv_row(p, btrow, L - si.nq + j) + static_cast<int64_t>(h) * p.c_shead;
-        kv = load4f<T>(p.kc + crow + d4);
-        vv = load4f<T>(p.vc + crow + d4);
-      }
-      float dot = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
 #pragma unroll
-      for (int off = 1; off < 32; off <<= 1) dot += __shfl_xor(dot, off);
-      const float sj = dot * p.scale_log2;
-      const float mn = fmaxf(M, sj);
-      const float r = sd::fast_exp2(M - mn), w = sd::fast_exp2(sj - mn);
-      l = l * r + w;
-      o = o * r + w * vv;
-      M = mn;
-    };
-    if (si.nq == 1) {  // decode: one new key (uniform over the row's lanes)
-      if (L - 1 >= 0) merge_new(0, to4f<T>(kb[0]), to4f<T>(vb[0]), sn[0]);
-    } else {
-      // several new keys: their unstored cache rows and their dot products first,
-      // the butterflies of all keys interleaved (each a chain of five dependent
-      // exchanges), then the merges in key order (the same operations in the
-      // same order as one key at a time)
-      bool use[NK];
-      float dot[NK];
-      f32x4 kn[NK], vn[NK];
-#pragma unroll
-      for (int j = 0; j < NK; ++j) {  // uniform over the row's lanes
-        kn[j] = to4f<T>(kb[j]);
-        vn[j] = to4f<T>(vb[j]);
-        use[j] = j < si.nq && j <= qi && L - si.nq + j >= 0;
-        if (use[j] && !(sn[j] >= 0 && sn[j] < p.num_slots)) {  // not stored: the cache row stays
-          const int64_t crow = kv_row(p, btrow, L - si.nq + j) + static_cast<int64_t>(h) * p.c_shead;
-          kn[j] = load4f<T>(p.kc + crow + d4);
-          vn[j] = load4f<T>(p.vc + crow + d4);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < NK; ++j)
-        dot[j] = use[j] ? qv.x * kn[j].x + qv.y * kn[j].y + qv.z * kn[j].z + qv.w * kn[j].w : 0.f;
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1)
-#pragma unroll
-        for (int j = 0; j < NK; ++j) dot[j] += __shfl_xor(dot[j], off);
-#pragma unroll
-      for (int j = 0; j < NK; ++j) {
-        if (!use[j]) continue;
-        const float sj = dot[j] * p.scale_log2;
-        const float mn = fmaxf(M, sj);
-        const float r = sd::fast_exp2(M - mn), w = sd::fast_exp2(sj - mn);
-        l = l * r + w;
-        o = o * r + w * vn[j];
-        M = mn;
-      }
-    }
+    for (int j = 0; j < NK; ++j)
+      if (j >= jlo && j <= jhi) merge_key(dot[j], to4f<T>(vb[j]));
+    // rows past NK (more new rows per sequence than the launch loads up front;
+    // only this row's lanes take part in the reductions from here on)
     for (int j = NK; j < si.nq; ++j) {
-      if (L - si.nq + j < 0 || j > qi) continue;
+      const bool u = j >= jlo && j <= jhi;  // uniform over the row's lanes
       const int64_t tr = si.q0 + j;
-      merge_new(j,
-                load4f<T>(p.knew + tr * p.kn_stok + static_cast<int64_t>(h) * p.kn_shead + d4),
-                load4f<T>(p.vnew + tr * p.vn_stok + static_cast<int64_t>(h) * p.vn_shead + d4),
-                p.slot[tr]);
+      uint2 kj = load_bits4(p.knew + tr * p.kn_stok + static_cast<int64_t>(h) * p.kn_shead + d4);
+      uint2 vj = load_bits4(p.vnew + tr * p.vn_stok + static_cast<int64_t>(h) * p.vn_shead + d4);
+      if (u && static_cast<uint32_t>(p.slot[tr]) >= ns32) {  // not stored: the cache row stays
+        const int64_t crow = kv_row(p, btrow, L - si.nq + j) + static_cast<int64_t>(h) * p.c_shead;
+        kj = load_bits4(p.kc + crow + d4);
+        vj = load_bits4(p.vc + crow + d4);
+      }
+      const float dj =
+          sd::half_wave_sum(u ? sd::dot2<T>(qb.y, kj.y, sd::dot2<T>(qb.x, kj.x, 0.f)) : 0.f);
+      if (u) merge_key(dj, to4f<T>(vj));
     }
   }
   store4<T>(op, o, l > 0.f ? 1.f / l : 0.f);

@@ -72,6 +72,15 @@ template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float 
 template <typename T> __device__ __forceinline__ float from_bits(uint16_t b) {
   return static_cast<float>(__builtin_bit_cast(T, b));
 }
+// acc + a.lo * b.lo + a.hi * b.hi over two packed 16-bit values (v_dot2c_f32_*:
+// the products are exact in fp32).
+template <typename T> __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  if constexpr (__is_same(T, __bf16))
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b),
+                                           acc, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
+}
 // Split two fp32 values into 16-bit hi parts and 16-bit parts of the remainder:
 // a = float(hi_a) + float(lo_a) to ~2^-17 relative (hi and lo each RNE).
 template <typename T>
@@ -180,6 +189,30 @@ __device__ __forceinline__ int wave_inclusive_sum(int x) {
   x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
   x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
   return x;
+}
+
+// v plus lane (DPP control CTRL)'s v; lanes whose source lane is outside its
+// row add 0.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                          0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each 32-lane half of the wave, the same value in all 32 lanes of the
+// half (every step adds two lanes' values, which commute): xor 1 and xor 2
+// inside quads, the mirrors inside 8 and 16 lanes, then the two 16-lane rows
+// of the half swapped (v_permlane16_swap) and added. A half whose lanes are all
+// inactive does not disturb the other.
+__device__ __forceinline__ float half_wave_sum(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  const auto z = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
+                                                  __builtin_bit_cast(uint32_t, v), false, false);
+  return __builtin_bit_cast(float, static_cast<uint32_t>(z[0])) +
+         __builtin_bit_cast(float, static_cast<uint32_t>(z[1]));
 }
 
 // 2^x on the transcendental unit (v_exp_f32) without denormal fix-ups:

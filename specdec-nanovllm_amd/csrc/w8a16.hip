@@ -938,12 +938,6 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
 #endif
 constexpr int kCycWgsPerCu = SD_W8_CYC_WGS_PER_CU;
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float v) {
-  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                          0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
 // a[0..3] per lane -> every lane of 16-lane row r holds the wave's sum of a[r]
 __device__ __forceinline__ float reduce4_rows(float a0, float a1, float a2, float a3) {
   // lanes 0-31 of a0 meet lanes 32-63 of a0 (and a2's halves the other way)
@@ -960,10 +954,10 @@ __device__ __forceinline__ float reduce4_rows(float a0, float a1, float a2, floa
                                             __builtin_bit_cast(uint32_t, s13), false, false);
   float v = __builtin_bit_cast(float, static_cast<uint32_t>(z[0])) +
             __builtin_bit_cast(float, static_cast<uint32_t>(z[1]));
-  v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v = dpp_add<0x141>(v);  // row_half_mirror
-  v = dpp_add<0x140>(v);  // row_mirror
+  v = sd::dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = sd::dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = sd::dpp_add<0x141>(v);  // row_half_mirror
+  v = sd::dpp_add<0x140>(v);  // row_mirror
   return v;
 }
 
