@@ -615,9 +615,11 @@ def bench_draft_chain(workloads_mod, torch, reps=5):
     """C5: hipGraph-captured k = 6 greedy draft steps of a random-init
     Qwen3-0.6B (28 layers, all linears W8A16, paged bf16 KV with a 2048-token
     context) at B in {1, 16}, with the neighbour ops as eager torch (the C5
-    protocol) and as this library's fused kernels: us per draft step,
-    algorithmic GB/s, and the shares of attention (store + paged attention) and
-    of the W8A16 GEMVs, each timed as its own graph over the same shapes."""
+    protocol) and as this library's fused kernels: us per draft step and
+    algorithmic GB/s. The fused rows' attention / GEMV split comes from a kernel
+    trace of the chain (`c5_kernel_split`); the graph-timed figures (attention =
+    store + paged attention, GEMV = the W8A16 linears, each captured as its own
+    graph over the same shapes) stay beside it as `*_graph_us`."""
     from specdec_nanovllm_amd.draft_chain import DraftChain
     rows = []
     for B in (1, 16):
@@ -637,16 +639,93 @@ def bench_draft_chain(workloads_mod, torch, reps=5):
                              + ("fused HIP kernels" if fused else "eager torch"),
                    "step_us": round(step, 2),
                    "step_minmax_us": [round(tt[1] * 1e3, 2), round(tt[2] * 1e3, 2)],
-                   "attention_us": round(parts["attention"], 2),
-                   "gemv_us": round(parts["gemv"], 2),
+                   "attention_graph_us": round(parts["attention"], 2),
+                   "gemv_graph_us": round(parts["gemv"], 2),
                    "GBps": round(ch.step_bytes() / step / 1e3, 1),
-                   "attention_share": round(parts["attention"] / step, 3),
-                   "gemv_share": round(parts["gemv"] / step, 3),
+                   "attention_graph_share": round(parts["attention"] / step, 3),
+                   "gemv_graph_share": round(parts["gemv"] / step, 3),
                    "bytes_per_step": ch.step_bytes()}
             rows.append(out)
         del ch
         torch.cuda.empty_cache()
+    for out in rows:
+        if out["config"].endswith("fused HIP kernels"):
+            B = int(out["config"].split("B=")[1].split()[0])
+            print(f"bench: C5 B={B} kernel trace (rocprofv3 child process)", file=sys.stderr,
+                  flush=True)
+            kt = c5_kernel_split(B)
+            out["kernel_trace"] = kt
+            if "error" not in kt:
+                out["attention_share"] = kt["attention_share"]
+                out["gemv_share"] = kt["gemv_share"]
     return rows
+
+
+TRACED_REPLAYS = 4  # chain replays between the markers of --draft-chain-only
+MARKER_KERNEL = "stream_read_kernel"
+
+
+def c5_kernel_split(B, timeout_s=240):
+    """The fused C5 chain's kernel time by class, from a kernel trace: this script
+    re-run as a child process under `rocprofv3 --kernel-trace` with
+    `--draft-chain-only B`, which replays the captured chain TRACED_REPLAYS times
+    between two launches of the streaming-read kernel (a kernel the chain never
+    launches); only the dispatches between the two markers count (no context
+    prefill, no setup). Attention = the q/k norm + RoPE + store launch and both
+    paged-attention launches; GEMV = every W8A16 launch (the decoder linears and
+    lm_head); other = the rest (norms, sampler, embedding lookup). Returns us per
+    draft step per class and the shares of the summed kernel time, or
+    {"error": ...}."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    tmp = tempfile.mkdtemp(prefix="c5trace_", dir="/tmp")
+    cmd = [prof, "--kernel-trace", "--output-format", "csv", "-d", tmp, "-o", "c5", "--",
+           sys.executable, os.path.abspath(__file__), "--draft-chain-only", str(B)]
+    try:
+        env = dict(os.environ, TMPDIR=tmp)
+        r = subprocess.run(cmd, cwd=tmp, env=env, stdout=subprocess.PIPE,
+                           stderr=subprocess.STDOUT, timeout=timeout_s, text=True)
+        info = None
+        for line in r.stdout.splitlines():
+            if line.startswith("{") and "draft_chain_only" in line:
+                info = json.loads(line)
+        trace = glob.glob(os.path.join(tmp, "**", "c5_kernel_trace.csv"), recursive=True)
+        if info is None or not trace:  # (rocprofv3 may end with 139 after whole results)
+            return {"error": f"rocprofv3 rc={r.returncode}: " + r.stdout[-300:]}
+        rows = sorted(((int(d["Start_Timestamp"]), int(d["End_Timestamp"]), d["Kernel_Name"])
+                       for d in csv.DictReader(open(trace[0]))), key=lambda t: t[0])
+        marks = [i for i, t in enumerate(rows) if MARKER_KERNEL in t[2]]
+        if len(marks) < 2:
+            return {"error": f"{len(marks)} marker dispatches in the trace"}
+        chain = rows[marks[-2] + 1:marks[-1]]
+        steps = info["traced_replays"] * info["steps_per_chain"]
+        mains = sum("paged_attn_main" in t[2] for t in chain)
+        if mains != steps * info["layers"]:
+            return {"error": f"{mains} attention launches between the markers, expected "
+                             f"{steps * info['layers']}"}
+        ns = {"attention": 0, "gemv": 0, "other": 0}
+        for t0, t1, name in chain:
+            cls = ("attention" if "paged_attn" in name or "qk_norm_rope" in name
+                   else "gemv" if "w8a16" in name else "other")
+            ns[cls] += t1 - t0
+        tot = sum(ns.values())
+        out = {"source": f"rocprofv3 --kernel-trace, {info['traced_replays']} replays of the "
+                         f"captured chain ({steps} draft steps, {len(chain)} dispatches)",
+               "kernel_us_per_step": round(tot / steps / 1e3, 2),
+               "launches_per_step": round(len(chain) / steps, 1),
+               "span_us_per_step": round((chain[-1][1] - chain[0][0]) / steps / 1e3, 2)}
+        for k, v in ns.items():
+            out[f"{k}_us"] = round(v / steps / 1e3, 2)
+            out[f"{k}_share"] = round(v / tot, 3) if tot else None
+        return out
+    except Exception as e:  # the split is a report; the bench line stands without it
+        return {"error": f"{type(e).__name__}: {e}"}
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
 
 
 # ---------------------------------------------------------------------------- profile
@@ -759,9 +838,21 @@ def main():
         g = graph_of(ch.chain, torch)
         step = time_replays([g], 5, 1, torch) * 1e3 / ch.k
         # the chain ran once eagerly before capture, then in the settle phase, once
-        # more and 5 timed times
+        # more and 5 timed times; then TRACED_REPLAYS more between two launches of
+        # the streaming-read kernel over 4 KiB, which the chain never launches: a
+        # kernel trace's dispatches between the two markers are these replays
+        marker = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+        sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+        ops.stream_read(marker, sink, 1)
+        torch.cuda.synchronize()
+        for _ in range(TRACED_REPLAYS):
+            g.replay()
+        torch.cuda.synchronize()
+        ops.stream_read(marker, sink, 1)
+        torch.cuda.synchronize()
         print(json.dumps({"draft_chain_only": args.draft_chain_only, "fused": True,
-                          "step_us": round(step, 2), "steps_per_chain": ch.k}), flush=True)
+                          "step_us": round(step, 2), "steps_per_chain": ch.k,
+                          "layers": ch.L, "traced_replays": TRACED_REPLAYS}), flush=True)
         return
 
     B = args.batch
