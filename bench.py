@@ -120,6 +120,22 @@ def settle(graph, torch, ms=SETTLE_MS):
     torch.cuda.synchronize()
 
 
+# Launches per timed graph: each per-call leg repeats its cycle of page sets or
+# weight copies until one graph holds at least this many. Replaying a graph costs
+# about 4 us on the GPU between its last kernel and the next replay's first (one
+# process, lm_head M = 1: 25.6 us per call with 4 calls per graph, 24.8 with 20,
+# 24.6 with 40), a gap a serving step's graph, which holds hundreds of launches,
+# amortizes; at 4-8 calls per graph it was charged to every call.
+MIN_GRAPH_CALLS = 40
+
+
+def cycle(fns, min_calls=MIN_GRAPH_CALLS):
+    """(body, calls): one graph body calling ``fns`` in turn, the cycle repeated
+    until it holds at least ``min_calls`` launches, and how many it holds."""
+    reps = max(1, math.ceil(min_calls / len(fns)))
+    return (lambda: [f() for _ in range(reps) for f in fns]), reps * len(fns)
+
+
 def time_groups(graph, per_replay, torch, groups=5, min_launches=20, warmup=2):
     """Per-launch time of the launches one replay of ``graph`` holds
     (``per_replay`` of them): after ``settle`` and ``warmup`` replays, HIP
@@ -400,23 +416,24 @@ def bench_verify(ops, workloads, torch, steps):
                                                tables[i], case["scale"], cu_seqlens_k=cuk,
                                                cu_seqlens_q=cuq, max_seqlen_q=case["k"] + 1,
                                                out=out, **kw)
-        fns = [one(i) for i in range(sets)]
-        return lambda: [f() for f in fns]
+        return cycle([one(i) for i in range(sets)])
     del steps
-    t = time_groups(graph_of(chain(True), torch), sets, torch)
+    body, calls = chain(True)
+    t = time_groups(graph_of(body, torch), calls, torch)
     ms = t[0]
     nbytes = (attn_bytes(case["keys"].tolist(), 32, 8, 128, 2, q_rows=case["k"] + 1)
               + case["slots"].numel() * 8 * 128 * 2 * 2 * 2)
     flops = sum(4 * 32 * 128 * (case["k"] + 1) * int(L) for L in case["keys"])
     res = {"config": f"C3 verify B=8 q_len 7 (store + attention), {sets} page sets, "
-                     f"{sets} calls per graph", "us": round(ms * 1e3, 2),
+                     f"{calls} calls per graph", "us": round(ms * 1e3, 2),
            "GBps": round(nbytes / ms / 1e6, 1), "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
            "TFLOPs": round(flops / ms / 1e9, 2), "seed": case["seed_used"],
            "algorithmic_bytes": nbytes, "minmax_us": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
            "timing": "median of 5 groups of >= 20 calls"}
     # the plain (non-storing) call and its twins over the same keys
     for twin, key in ((None, "attention_us"), ("main", "main_us"), ("floor", "floor_us")):
-        tt = time_groups(graph_of(chain(False, twin), torch), sets, torch)
+        body, calls = chain(False, twin)
+        tt = time_groups(graph_of(body, torch), calls, torch)
         res[key] = round(tt[0] * 1e3, 2)
         res[key.replace("_us", "_minmax_us")] = [round(tt[1] * 1e3, 2), round(tt[2] * 1e3, 2)]
     return res
@@ -449,14 +466,16 @@ def bench_decode_batch(ops, workloads, torch, B, steps):
                                                            {"twin": kw.get("twin"),
                                                             "workspace": ws}))
                for i in range(sets)]
-        return lambda: [f() for f in fns]
+        return cycle(fns)
     del steps
-    res = {"config": f"C2 decode step B={B} (store + attention), {sets} page sets, median of "
-                     "5 groups of >= 20 calls"}
+    res = {"config": f"C2 decode step B={B} (store + attention), {sets} page sets cycled "
+                     f"through >= {MIN_GRAPH_CALLS} calls per graph, median of 5 groups of "
+                     ">= 20 calls"}
     for name, kw in (("step_us", {"store": True}), ("attention_us", {}),
                      ("main_us", {"twin": "main"}), ("floor_us", {"twin": "floor"})):
-        g = graph_of(chain(**kw), torch)
-        t = time_groups(g, sets, torch)
+        body, calls = chain(**kw)
+        g = graph_of(body, torch)
+        t = time_groups(g, calls, torch)
         res[name] = round(t[0] * 1e3, 2)
         res[name.replace("_us", "_minmax_us")] = [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)]
         del g
@@ -489,18 +508,18 @@ def bench_ctx_sweep(ops, workloads, torch):
 
         def chain(store):
             if store:
-                return lambda: [ops.paged_attention(case["q"], case["k_cache"], case["v_cache"],
-                                                    tables[i], case["scale"], context_lens=lens,
-                                                    out=out, key=case["k_new"],
-                                                    value=case["v_new"], slot_mapping=slots[i])
-                                for i in range(sets)]
-            return lambda: [ops.paged_attention(case["q"], case["k_cache"], case["v_cache"],
-                                                tables[i], case["scale"], context_lens=lens,
-                                                out=out, workspace=ws) for i in range(sets)]
+                return cycle([lambda i=i: ops.paged_attention(
+                    case["q"], case["k_cache"], case["v_cache"], tables[i], case["scale"],
+                    context_lens=lens, out=out, key=case["k_new"], value=case["v_new"],
+                    slot_mapping=slots[i]) for i in range(sets)])
+            return cycle([lambda i=i: ops.paged_attention(
+                case["q"], case["k_cache"], case["v_cache"], tables[i], case["scale"],
+                context_lens=lens, out=out, workspace=ws) for i in range(sets)])
         row = {"ctx": L}
         for key, store in (("attention_us", False), ("step_us", True)):
-            g = graph_of(chain(store), torch)
-            t = time_groups(g, sets, torch, groups=5, min_launches=32)
+            body, calls = chain(store)
+            g = graph_of(body, torch)
+            t = time_groups(g, calls, torch, groups=5, min_launches=32)
             del g
             row[key] = round(t[0] * 1e3, 2)
             row[key.replace("_us", "_minmax_us")] = [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)]
@@ -513,31 +532,55 @@ def bench_ctx_sweep(ops, workloads, torch):
                       "median of 5 groups of >= 32 calls", "rows": rows}
 
 
-def bench_w8a16(ops, workloads, torch, steps):
-    """Each shape x M: one HIP graph holding a chain of calls over `copies`
-    distinct weight copies (> 2 x the 256 MB MALL in total, so every call
-    streams its weight from HBM, as a model forward does); us per call = the
-    median over 5 groups of >= 20 calls (min / max beside it). Beside each
-    row: the load-only twin (sd_w8a16_floor, same plan and loads, no math) and,
-    at M in {1, 16}, the dense bf16 linear torch runs for the same shape
-    (F.linear, hipBLASLt) over bf16 weight copies, as the reference compares
-    its int8 path with the bf16 GEMM (docs/W8A16量化-开发记录.md:264-275,
-    scripts/bench_int8_gemm.py:138-146)."""
+def preload_w8a16(workloads, torch):
+    """The C4 weights, allocated first in the process, as a serving process loads
+    its weights before it allocates its KV cache: per shape, `copies` distinct
+    int8 weight copies (> 2 x the 256 MB MALL in total, so every call streams its
+    weight from HBM, as a model forward does) with their per-channel scale, and
+    the bf16 copies of the dense comparison. The same weights allocated after a
+    large allocate-and-free read measurably slower (one process, lm_head: 25.8
+    against 24.5 us per call at M = 1, 30.0 against 28.7 at M = 16, after an
+    8 GB allocate-and-free), which a bench that frees its attention buffers first
+    would charge to the kernel."""
+    pre = {}
+    for name, N, K in workloads.W8A16_SHAPES:
+        copies = max(2, math.ceil(2 * 256e6 / (N * K)))
+        base = workloads.w8a16_case(1, N, K, seed=N)
+        ws = [base["w"]] + [torch.roll(base["w"], i, 0) for i in range(1, copies)]
+        bcopies = max(2, math.ceil(2 * 256e6 / (2 * N * K)))
+        gen = torch.Generator(device="cuda").manual_seed(N + K)
+        wb = [(torch.randn((N, K), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+              for _ in range(bcopies)]
+        pre[name] = {"ws": ws, "s": base["s"], "wb": wb}
+    torch.cuda.synchronize()
+    return pre
+
+
+def bench_w8a16(ops, workloads, torch, steps, pre):
+    """Each shape x M: one HIP graph holding a chain of calls cycling over the
+    preloaded weight copies (`preload_w8a16`); us per call = the median over 5
+    groups of >= 20 calls (min / max beside it). Beside each row: the load-only
+    twin (sd_w8a16_floor, same plan and loads, no math) and, at M in {1, 16}, the
+    dense bf16 linear torch runs for the same shape (F.linear, hipBLASLt) over
+    bf16 weight copies, as the reference compares its int8 path with the bf16
+    GEMM (docs/W8A16量化-开发记录.md:264-275, scripts/bench_int8_gemm.py:138-146)."""
     import torch.nn.functional as F
     rows = []
     del steps
     for name, N, K in workloads.W8A16_SHAPES:
         for M in workloads.W8A16_MS:
-            copies = max(2, math.ceil(2 * 256e6 / (N * K)))
-            base = workloads.w8a16_case(M, N, K, seed=N + M)
-            ws = [base["w"]] + [torch.roll(base["w"], i, 0) for i in range(1, copies)]
+            ws = pre[name]["ws"]
+            g = torch.Generator(device="cuda").manual_seed(N + M)
+            base = {"s": pre[name]["s"],
+                    "x": torch.randn((M, K), generator=g, device="cuda").to(torch.float16)}
             y = torch.empty((M, N), dtype=torch.float16, device="cuda")
             nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
             row = {"shape": name, "M": M, "N": N, "K": K}
             for key, twin in (("us", None), ("floor", "floor")):
-                g = graph_of(lambda: [ops.w8a16_linear(base["x"], w, base["s"], out=y, twin=twin)
-                                      for w in ws], torch)
-                t = time_groups(g, copies, torch)
+                body, calls = cycle([lambda w=w: ops.w8a16_linear(base["x"], w, base["s"],
+                                                                  out=y, twin=twin) for w in ws])
+                g = graph_of(body, torch)
+                t = time_groups(g, calls, torch)
                 del g
                 if twin is None:
                     row.update(us3(t))
@@ -545,17 +588,13 @@ def bench_w8a16(ops, workloads, torch, steps):
                     row["frac"] = round(nbytes / t[0] / 1e6 / PEAK_HBM_GBS, 4)
                 else:
                     row["floor_us"] = round(t[0] * 1e3, 2)
-            del ws
-            torch.cuda.empty_cache()
             if M in (1, 16):
-                bcopies = max(2, math.ceil(2 * 256e6 / (2 * N * K)))
-                gen = torch.Generator(device="cuda").manual_seed(N + K)
-                wb = [(torch.randn((N, K), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
-                      for _ in range(bcopies)]
+                wb = pre[name]["wb"]
                 xb = base["x"].to(torch.bfloat16)
                 try:
-                    g = graph_of(lambda: [F.linear(xb, w) for w in wb], torch)
-                    t = time_groups(g, bcopies, torch)
+                    body, calls = cycle([lambda w=w: F.linear(xb, w) for w in wb])
+                    g = graph_of(body, torch)
+                    t = time_groups(g, calls, torch)
                     del g
                     bbytes = 2 * N * K + 2 * M * K + 2 * M * N
                     row["bf16_linear_us"] = round(t[0] * 1e3, 2)
@@ -564,8 +603,6 @@ def bench_w8a16(ops, workloads, torch, steps):
                 except RuntimeError as e:  # capture refused: say so, no number
                     row["bf16_linear_us"] = None
                     row["bf16_linear_note"] = str(e)[:120]
-                del wb
-                torch.cuda.empty_cache()
             rows.append(row)
             del base
     return rows
@@ -611,7 +648,16 @@ def bench_prefill(ops, torch, steps):
             "frac_of_bf16_peak": round(flops / ms / 1e9 / 2500.0, 4)}
 
 
-def bench_draft_chain(workloads_mod, torch, reps=5):
+def preload_draft_chains(torch):
+    """The C5 draft models (weights, then their paged KV caches) for B in {1, 16},
+    built first in the process with the C4 weights (see `preload_w8a16`)."""
+    from specdec_nanovllm_amd.draft_chain import DraftChain
+    chains = {B: DraftChain(B, ctx_len=2048, k=6, seed=B) for B in (1, 16)}
+    torch.cuda.synchronize()
+    return chains
+
+
+def bench_draft_chain(workloads_mod, torch, chains, reps=5):
     """C5: hipGraph-captured k = 6 greedy draft steps of a random-init
     Qwen3-0.6B (28 layers, all linears W8A16, paged bf16 KV with a 2048-token
     context) at B in {1, 16}, with the neighbour ops as eager torch (the C5
@@ -620,10 +666,9 @@ def bench_draft_chain(workloads_mod, torch, reps=5):
     trace of the chain (`c5_kernel_split`); the graph-timed figures (attention =
     store + paged attention, GEMV = the W8A16 linears, each captured as its own
     graph over the same shapes) stay beside it as `*_graph_us`."""
-    from specdec_nanovllm_amd.draft_chain import DraftChain
     rows = []
     for B in (1, 16):
-        ch = DraftChain(B, ctx_len=2048, k=6, seed=B)
+        ch = chains.pop(B)
         parts = {}
         for name, fn in (("attention", ch.attention_chain), ("gemv", ch.gemv_chain)):
             g = graph_of(fn, torch)
@@ -869,6 +914,12 @@ def main():
     slots = [s.cuda() for s in case["slots"]]
     kc, vc, q = case["k_cache"], case["v_cache"], case["q"]
     out = torch.empty_like(q)
+    # the extras' weights (C4 copies, C5 draft models) right after the headline's
+    # KV cache and before anything is freed: both allocations are fresh, as in a
+    # serving process, which loads its weights and allocates its KV cache once
+    w8_pre = preload_w8a16(workloads, torch) if not args.no_extra else None
+    c5_pre = (preload_draft_chains(torch)
+              if not args.no_extra and not args.no_draft_chain else None)
 
     def step_fn(i):
         # store_kvcache of the new rows + attention: one fused launch (+ combine)
@@ -903,10 +954,12 @@ def main():
     step_graphs = [graph_of(step_fn(i), torch) for i in range(sets)]
 
     def chain(make):
-        # one graph launching the kernel once per page set: back-to-back launches
-        # with no host gap between them, each on cold (not yet read) pages
-        fns = [make(i) for i in range(sets)]
-        return lambda: [f() for f in fns]
+        # one graph launching the kernel once per page set, the cycle repeated to
+        # >= MIN_GRAPH_CALLS launches: back-to-back launches with no host gap
+        # between them, each on cold pages (the other sets stream more than the
+        # MALL holds before a set comes back)
+        return cycle([make(i) for i in range(sets)])[0]
+    roof_calls = cycle([None] * sets)[1]
     main_graphs = [graph_of(chain(main_fn), torch)]
     attn_graphs = [graph_of(chain(attn_fn), torch)]
     floor_graphs = [graph_of(chain(floor_fn), torch)]
@@ -933,10 +986,10 @@ def main():
     # ---- dominant kernel: attention main kernel alone, HIP events on the launching
     #      (current) stream around graph chains of back-to-back launches: the median
     #      of 5 groups of >= 20 launches, whatever --steps is (min / max beside it)
-    t_main = time_groups(main_graphs[0], sets, torch)
-    t_attn = time_groups(attn_graphs[0], sets, torch)
-    t_floor = time_groups(floor_graphs[0], sets, torch)
-    t_comb = time_groups(combine_graphs[0], sets, torch)
+    t_main = time_groups(main_graphs[0], roof_calls, torch)
+    t_attn = time_groups(attn_graphs[0], roof_calls, torch)
+    t_floor = time_groups(floor_graphs[0], roof_calls, torch)
+    t_comb = time_groups(combine_graphs[0], roof_calls, torch)
     ms_main, ms_attn, ms_floor, ms_comb = t_main[0], t_attn[0], t_floor[0], t_comb[0]
     a_bytes = attn_bytes(lens.tolist(), hq, hkv, d, 2)
     achieved = a_bytes / (ms_main * 1e-3) / 1e9
@@ -962,8 +1015,9 @@ def main():
                      "kernel": "paged_attn_main", "algorithmic_bytes": a_bytes,
                      "avg_us": round(ms_main * 1e3, 2),
                      "avg_minmax_us": [round(t_main[1] * 1e3, 2), round(t_main[2] * 1e3, 2)],
-                     "timing": "median of 5 groups of >= 20 launches (graph chains over "
-                               f"{sets} page sets), HIP events on the launching stream",
+                     "timing": "median of 5 groups of >= 20 launches (graph chains of "
+                               f"{roof_calls} launches cycling over {sets} page sets), HIP "
+                               "events on the launching stream",
                      "floor_us": round(ms_floor * 1e3, 2),
                      "floor_minmax_us": [round(t_floor[1] * 1e3, 2),
                                          round(t_floor[2] * 1e3, 2)],
@@ -997,7 +1051,8 @@ def main():
         torch.cuda.empty_cache()
         extra["verify"] = bench_verify(ops, workloads, torch, args.steps)
         torch.cuda.empty_cache()
-        extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100))
+        extra["w8a16"] = bench_w8a16(ops, workloads, torch, min(args.steps, 100), w8_pre)
+        del w8_pre
         if not args.no_cpu_baseline:
             extra["cpu_baselines"] = cpu_baselines_extra(torch, workloads,
                                                          workloads.verify_case(seed=0))
@@ -1008,7 +1063,7 @@ def main():
         extra["prefill"] = bench_prefill(ops, torch, min(args.steps, 50))
         torch.cuda.empty_cache()
         if not args.no_draft_chain:
-            extra["draft_chain"] = bench_draft_chain(workloads, torch)
+            extra["draft_chain"] = bench_draft_chain(workloads, torch, c5_pre)
         line["extra"] = extra
     print(json.dumps(line), flush=True)
 
