@@ -236,6 +236,13 @@ __device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_
   constexpr int kChunks = 4;
   float v[kChunks][8];
   float ss = 0.f;
+  // the weight's chunks load with the row's (one round trip, not one after the sum)
+  u32x4 wq[kChunks];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e0 = (c * 256 + static_cast<int>(threadIdx.x)) * 8;
+    wq[c] = threadIdx.x < 256 && e0 < H ? load16(w + e0) : u32x4{0u, 0u, 0u, 0u};
+  }
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
     const int e0 = (c * 256 + static_cast<int>(threadIdx.x)) * 8;
@@ -268,7 +275,7 @@ __device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_
   for (int c = 0; c < kChunks; ++c) {
     const int e0 = (c * 256 + static_cast<int>(threadIdx.x)) * 8;
     if (threadIdx.x < 256 && e0 < H) {
-      const u32x4 wv = load16(w + e0);
+      const u32x4 wv = wq[c];
       const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
       uint32_t o[4], ro[4];
 #pragma unroll
