@@ -92,7 +92,8 @@ template <typename T>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(RopeParams p) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) +
+                       __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int heads = p.Hq + p.Hkv;
   if (item >= p.tokens * heads) return;
   const int64_t t = item / heads;
@@ -101,33 +102,49 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(RopeParams p) {
   uint16_t* x = is_q ? p.q + t * p.q_stok + static_cast<int64_t>(hd) * p.q_shead
                      : p.k + t * p.k_stok + static_cast<int64_t>(hd - p.Hq) * p.k_shead;
   const uint16_t* w = is_q ? p.qw : p.kw;
-  const int64_t pos = p.pos[t];
-  // k heads of a fused store: the row's cache slot (-1 or outside the pool:
-  // not written, as store_kvcache)
+  const bool store = p.kc && !is_q;  // k heads of a fused store_kvcache
+  // Every load that depends on nothing else goes out first, unconditionally
+  // (absent operands read a valid stand-in, never used): the position, the
+  // slot, the head's two elements, the norm weight's and the value row's.
+  // Then the cos / sin row at the position. Loads under branches or after the
+  // reduction cost this small kernel one dependent round trip each.
+  const uint16_t* wsrc = w ? w : x;
+  const uint16_t* vsrc = store ? p.v + t * p.v_stok + static_cast<int64_t>(hd - p.Hq) * p.v_shead : x;
+  // the token index in a VGPR: position and slot become vector loads, counted
+  // in order with the rest (scalar loads return out of order, so the first use
+  // of any kernel argument after them would wait for them)
+  int64_t tv = t;
+  asm volatile("" : "+v"(tv));
+  const int32_t* ssrc = p.slot ? p.slot + tv : reinterpret_cast<const int32_t*>(p.pos + tv);
+  const int64_t pos = p.pos[tv];
+  const int64_t sl = *ssrc;
+  const uint16_t xb0 = x[lane], xb1 = x[lane + 64];
+  const uint16_t wb0 = wsrc[lane], wb1 = wsrc[lane + 64];
+  const uint16_t vb0 = vsrc[lane], vb1 = vsrc[lane + 64];
+  const bool rope = pos >= 0 && pos < p.max_pos;  // no cos/sin row: the head is left as it is
+  const float* cs = p.cos_sin + (rope ? pos : 0) * p.cs_stride;
+  const float c = cs[lane], sn = cs[64 + lane];
+  // the row's cache slot (-1 or outside the pool: not written, as store_kvcache)
   uint16_t* kdst = nullptr;
   uint16_t* vdst = nullptr;
-  if (p.kc && !is_q) {
-    const int64_t sl = p.slot[t];
-    if (sl >= 0 && sl < p.num_slots) {
-      const int64_t blk = sl / p.block_size, off = sl - blk * p.block_size;
-      const int64_t row = blk * p.c_sblk + off * p.c_spos + static_cast<int64_t>(hd - p.Hq) * p.c_shead;
-      kdst = p.kc + row;
-      vdst = p.vc + row;
-      const uint16_t* vs = p.v + t * p.v_stok + static_cast<int64_t>(hd - p.Hq) * p.v_shead;
-      vdst[lane] = vs[lane];
-      vdst[lane + 64] = vs[lane + 64];
-    }
+  if (store && sl >= 0 && sl < p.num_slots) {
+    const int64_t blk = sl / p.block_size, off = sl - blk * p.block_size;
+    const int64_t row = blk * p.c_sblk + off * p.c_spos + static_cast<int64_t>(hd - p.Hq) * p.c_shead;
+    kdst = p.kc + row;
+    vdst = p.vc + row;
+    vdst[lane] = vb0;
+    vdst[lane + 64] = vb1;
   }
-  if (pos < 0 || pos >= p.max_pos) {  // no cos/sin row: the head is left as it is
+  if (!rope) {
     if (kdst) {
-      kdst[lane] = x[lane];
-      kdst[lane + 64] = x[lane + 64];
+      kdst[lane] = xb0;
+      kdst[lane + 64] = xb1;
     }
     return;
   }
   uint16_t lo, hi;
-  sd::head_norm_rope<T>(ld<T>(x, lane), ld<T>(x, lane + 64), w, p.eps,
-                        p.cos_sin + pos * p.cs_stride, lo, hi);
+  sd::head_norm_rope<T>(sd::from_bits<T>(xb0), sd::from_bits<T>(xb1), w != nullptr,
+                        sd::from_bits<T>(wb0), sd::from_bits<T>(wb1), p.eps, c, sn, lo, hi);
   x[lane] = lo;
   x[lane + 64] = hi;
   if (kdst) {

@@ -294,27 +294,27 @@ __device__ __forceinline__ void add_rmsnorm_row(const uint16_t* x, const uint16_
 }
 
 // One wave, one 128-element head (lane l holds elements l and l + 64 as x0,
-// x1): RMSNorm with `w` (NULL: none; the squares summed per lane, then xor
-// steps 32 .. 1), then rotate-half RoPE with the fp32 row cs = [cos(64) |
-// sin(64)]; returns the two outputs' 16-bit bits (lo: element l, hi: l + 64).
+// x1): RMSNorm with the weight's elements w0, w1 (has_w false: none; the
+// squares summed per lane, then xor steps 32 .. 1), then rotate-half RoPE with
+// this lane's cos c and sin s of the position; returns the two outputs' 16-bit
+// bits (lo: element l, hi: l + 64). Every operand arrives as a value, so the
+// caller issues all of its loads before the reduction.
 // Qwen3Attention's q_norm / k_norm then RotaryEmbedding.forward
 // (nanovllm/models/qwen3.py:80-88, layers/rotary_embedding.py:6-48), every
 // rounding of the eager module kept.
 template <typename T>
-__device__ __forceinline__ void head_norm_rope(float x0, float x1, const uint16_t* w, float eps,
-                                               const float* cs, uint16_t& lo, uint16_t& hi) {
+__device__ __forceinline__ void head_norm_rope(float x0, float x1, bool has_w, float w0, float w1,
+                                               float eps, float c, float s, uint16_t& lo,
+                                               uint16_t& hi) {
 #pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63;
-  if (w) {
+  if (has_w) {
     float ss = x0 * x0 + x1 * x1;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
     const float r = rsqrtf(ss / 128.f + eps);
-    x0 = static_cast<float>(round16<T>(static_cast<float>(round16<T>(x0 * r)) * from_bits<T>(w[lane])));
-    x1 = static_cast<float>(round16<T>(static_cast<float>(round16<T>(x1 * r)) * from_bits<T>(w[lane + 64])));
+    x0 = static_cast<float>(round16<T>(static_cast<float>(round16<T>(x0 * r)) * w0));
+    x1 = static_cast<float>(round16<T>(static_cast<float>(round16<T>(x1 * r)) * w1));
   }
-  const float c = cs[lane];
-  const float s = cs[64 + lane];
   const float a = x0 * c, b = x1 * s;
   const float e = x1 * c, f = x0 * s;
   lo = to_bits<T>(a - b);
