@@ -215,6 +215,39 @@ __device__ __forceinline__ float half_wave_sum(float v) {
          __builtin_bit_cast(float, static_cast<uint32_t>(z[1]));
 }
 
+// The xor butterfly `for (off = TOP; off > 0; off >>= 1) v += __shfl_xor(v, off)`
+// (TOP 32 or 16; the whole wave active) without LDS, bit for bit: each step
+// adds, in every lane l, v[l] and v[l ^ off] (a + b and b + a are the same
+// float). xor 32 and xor 16 are v_permlane32_swap / v_permlane16_swap of v
+// with itself (the two outputs of a lane are its own and its partner's
+// value), xor 8 rotates each 16-lane row by 8. A row then repeats with period
+// 8, so its rotation by 4 brings lane l ^ 4's value to lane l; xor 2 and xor 1
+// are quad permutations.
+template <int TOP>
+__device__ __forceinline__ float xor_sum_down(float v) {
+  static_assert(TOP == 32 || TOP == 16, "xor butterfly from lane distance 32 or 16");
+  if constexpr (TOP == 32) {
+    const auto z = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                    __builtin_bit_cast(uint32_t, v), false, false);
+    v = __builtin_bit_cast(float, static_cast<uint32_t>(z[0])) +
+        __builtin_bit_cast(float, static_cast<uint32_t>(z[1]));
+  }
+  const auto z = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
+                                                  __builtin_bit_cast(uint32_t, v), false, false);
+  v = __builtin_bit_cast(float, static_cast<uint32_t>(z[0])) +
+      __builtin_bit_cast(float, static_cast<uint32_t>(z[1]));
+  v = dpp_add<0x128>(v);  // row_ror:8
+  v = dpp_add<0x124>(v);  // row_ror:4
+  v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  return v;
+}
+
+// v of lane l (a wave-uniform l), as a uniform value
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
 // 2^x on the transcendental unit (v_exp_f32) without denormal fix-ups:
 // results below 2^-126 flush to 0, 2^-inf = 0. Softmax weights only.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

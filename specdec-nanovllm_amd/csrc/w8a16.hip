@@ -611,61 +611,87 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
   }
 }
 
-// Lane `lane`'s activations of the row-streaming kernels: xv[m][c][j] is column
-// c * 1024 + 16 lane + j of activation row m (zero past K or M). MODE 1 forms
-// SiluAndMul (silu_mul8, the SiLU kernel's element function), MODE 2 add +
-// RMSNorm with the RMSNorm kernel's summation order; `writer` (one wave of
-// the grid) stores the new residual.
+// Lane `lane`'s activations of the row-streaming kernels, in two steps so that
+// the caller's first weight loads go out between them: act_load issues every
+// load the activations need, with no branch (row and column clamped into the
+// matrix; K is a multiple of 8), and act_form forms xv[m][c][j], column
+// c * 1024 + 16 lane + j of activation row m (zero past K or M), selecting the
+// zeros once the data are in. A load under a per-lane bounds branch would be
+// waited for where its branch ends, with every load issued before it: one
+// round trip per branch. MODE 1 forms SiluAndMul (silu_mul8, the SiLU kernel's
+// element function), MODE 2 add + RMSNorm with the RMSNorm kernel's summation
+// order; `writer` (one wave of the grid) stores the new residual.
+template <int MR, int C, int MODE>
+struct RowActs {
+  static constexpr int MB = MODE == 0 ? 1 : MR, CB = MODE == 0 ? 1 : C, CN = MODE == 2 ? C : 1;
+  u32x4 a[MR][C][2];   // x (MODE 1: the gate half)
+  u32x4 b[MB][CB][2];  // MODE 1: the up half; MODE 2: the residual (x again without one)
+  u32x4 nw[CN][2];     // MODE 2: the norm weight
+};
+
+template <int MR, int C, int MODE>
+__device__ __forceinline__ void act_load(const W8Params& p, int lane, RowActs<MR, C, MODE>& r) {
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const int64_t mc = min(m, p.M - 1);
+    const uint16_t* xr = p.x + mc * p.xs;
+    const uint16_t* br = xr;
+    if constexpr (MODE == 1) br = xr + p.up;
+    if constexpr (MODE == 2) br = p.nres ? p.nres + mc * p.nres_s : xr;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int k = min(c * 1024 + 16 * lane + 8 * e, p.K - 8);
+        r.a[m][c][e] = sd::load16(xr + k);
+        if constexpr (MODE != 0) r.b[m][c][e] = sd::load16(br + k);
+      }
+  }
+  if constexpr (MODE == 2) {
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) r.nw[c][e] = sd::load16(p.nw + min(c * 1024 + 16 * lane + 8 * e, p.K - 8));
+  }
+}
+
 template <typename T, int MR, int C, int MODE>
-__device__ __forceinline__ void row_activations(const W8Params& p, int lane, bool writer,
-                                                float (&xv)[MR][C][16]) {
+__device__ __forceinline__ void act_form(const W8Params& p, int lane, bool writer,
+                                         const RowActs<MR, C, MODE>& r, float (&xv)[MR][C][16]) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     const bool mok = m < p.M;
-    const uint16_t* xr = p.x + static_cast<int64_t>(mok ? m : 0) * p.xs;
     if constexpr (MODE == 2) {
       // s = x (+ residual) in fp32; the RMSNorm kernel's thread t holds the
       // 8-column chunks t, t + 256, ..., so chunk 128 c + 2 lane + e (e = 0, 1)
       // is thread 128 (c % 2) + 2 lane + e: lane halves < 32 / >= 32 are its
       // waves 0 / 1 (even c) and 2 / 3 (odd c), and its xor steps 32 .. 2
       // are lane xor 16 .. 1 here, step 1 the e pair
+      const bool res = p.nres != nullptr;
       float ss[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [c % 2][e]
-      // the norm weight's columns load with the activations (one round trip)
-      u32x4 nwq[C][2];
-#pragma unroll
-      for (int c = 0; c < C; ++c)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int k0 = c * 1024 + 16 * lane + 8 * e;
-          nwq[c][e] = k0 < p.K ? sd::load16(p.nw + k0) : u32x4{0u, 0u, 0u, 0u};
-        }
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const int k0 = c * 1024 + 16 * lane;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          if (k0 + 8 * e < p.K) {
-            const u32x4 a = sd::load16(xr + k0 + 8 * e);
-            u32x4 bq = {0u, 0u, 0u, 0u};
-            if (p.nres) bq = sd::load16(p.nres + static_cast<int64_t>(m) * p.nres_s + k0 + 8 * e);
-            const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {bq.x, bq.y, bq.z, bq.w};
+          const bool ok = mok && k0 + 8 * e < p.K;
+          const u32x4 a = r.a[m][c][e], bq = r.b[m][c][e];
+          const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {bq.x, bq.y, bq.z, bq.w};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              float f = sd::from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
-              if (p.nres) f = f + sd::from_bits<T>(static_cast<uint16_t>(bw[i / 2] >> (16 * (i & 1))));
-              xv[m][c][8 * e + i] = f;
-              ss[c & 1][e] += f * f;
-            }
-            if (p.nres_out && writer && mok) {
-              uint32_t ro[4];
+          for (int i = 0; i < 8; ++i) {
+            const float f = sd::from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
+            const float g = sd::from_bits<T>(static_cast<uint16_t>(bw[i / 2] >> (16 * (i & 1))));
+            const float s = res ? f + g : f;
+            xv[m][c][8 * e + i] = ok ? s : 0.f;
+            ss[c & 1][e] += xv[m][c][8 * e + i] * xv[m][c][8 * e + i];  // + 0 past K
+          }
+          if (p.nres_out && writer && ok) {
+            uint32_t ro[4];
 #pragma unroll
-              for (int i = 0; i < 4; ++i) ro[i] = sd::pack2<T>(xv[m][c][8 * e + 2 * i], xv[m][c][8 * e + 2 * i + 1]);
-              sd::store16(p.nres_out + static_cast<int64_t>(m) * p.nres_out_s + k0 + 8 * e,
-                          u32x4{ro[0], ro[1], ro[2], ro[3]});
-            }
-          } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) xv[m][c][8 * e + i] = 0.f;
+            for (int i = 0; i < 4; ++i) ro[i] = sd::pack2<T>(xv[m][c][8 * e + 2 * i], xv[m][c][8 * e + 2 * i + 1]);
+            sd::store16(p.nres_out + static_cast<int64_t>(m) * p.nres_out_s + k0 + 8 * e,
+                        u32x4{ro[0], ro[1], ro[2], ro[3]});
           }
         }
       }
@@ -673,31 +699,30 @@ __device__ __forceinline__ void row_activations(const W8Params& p, int lane, boo
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int e = 0; e < 2; ++e)
-#pragma unroll
-          for (int off = 16; off > 0; off >>= 1) ss[h][e] += __shfl_xor(ss[h][e], off);
+        for (int e = 0; e < 2; ++e) ss[h][e] = sd::xor_sum_down<16>(ss[h][e]);
         wsum[h] = ss[h][0] + ss[h][1];
       }
+      // the RMSNorm kernel's waves 0 - 3, in order
       float tot = 0.f;
-      tot += __shfl(wsum[0], 0);
-      tot += __shfl(wsum[0], 32);
-      tot += __shfl(wsum[1], 0);
-      tot += __shfl(wsum[1], 32);
+      tot += sd::lane_value(wsum[0], 0);
+      tot += sd::lane_value(wsum[0], 32);
+      tot += sd::lane_value(wsum[1], 0);
+      tot += sd::lane_value(wsum[1], 32);
       const float rn = rsqrtf(tot / static_cast<float>(p.K) + p.neps);
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const int k0 = c * 1024 + 16 * lane;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          if (k0 + 8 * e < p.K) {
-            const u32x4 wq = nwq[c][e];
-            const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+          const bool ok = mok && k0 + 8 * e < p.K;
+          const u32x4 wq = r.nw[c][e];
+          const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const float n = static_cast<float>(sd::round16<T>(xv[m][c][8 * e + i] * rn));
-              const float wv = sd::from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> (16 * (i & 1))));
-              xv[m][c][8 * e + i] = static_cast<float>(sd::round16<T>(n * wv));
-            }
+          for (int i = 0; i < 8; ++i) {
+            const float n = static_cast<float>(sd::round16<T>(xv[m][c][8 * e + i] * rn));
+            const float wv = sd::from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> (16 * (i & 1))));
+            const float o = static_cast<float>(sd::round16<T>(n * wv));
+            xv[m][c][8 * e + i] = ok ? o : 0.f;
           }
         }
       }
@@ -707,15 +732,15 @@ __device__ __forceinline__ void row_activations(const W8Params& p, int lane, boo
         const int k0 = c * 1024 + 16 * lane;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          u32x4 a = {0u, 0u, 0u, 0u};
-          if (mok && k0 + 8 * e < p.K) {
-            a = sd::load16(xr + k0 + 8 * e);
-            if constexpr (MODE == 1) a = sd::silu_mul8<T>(a, sd::load16(xr + p.up + k0 + 8 * e));
-          }
+          const bool ok = mok && k0 + 8 * e < p.K;
+          u32x4 a = r.a[m][c][e];
+          if constexpr (MODE == 1) a = sd::silu_mul8<T>(a, r.b[m][c][e]);
           const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-          for (int i = 0; i < 8; ++i)
-            xv[m][c][8 * e + i] = sd::from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
+          for (int i = 0; i < 8; ++i) {
+            const float f = sd::from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
+            xv[m][c][8 * e + i] = ok ? f : 0.f;
+          }
         }
       }
     }
@@ -808,12 +833,14 @@ __global__ __launch_bounds__(kThreads) void w8a16_rows_kernel(W8Params p, int ro
     const uint16_t h = static_cast<uint16_t>(B.s0);
     return p.scale_dtype == SD_BF16 ? sd::from_bits<__bf16>(h) : sd::from_bits<_Float16>(h);
   };
+  // ---- this lane's activations (xv[m][c][j] = column c * 1024 + 16 lane + j),
+  // loaded ahead of the first batch and formed while it is in flight
+  RowActs<MR, C, MODE> ra;
+  act_load<MR, C, MODE>(p, lane, ra);
   Batch ba, bb;
-  load(ba, base(0));  // before the activations, so that their latencies overlap
-
-  // ---- this lane's activations: xv[m][c][j] = column c * 1024 + 16 lane + j
+  load(ba, base(0));
   float xv[MR][C][16];
-  row_activations<T, MR, C, MODE>(p, lane, gw == 0, xv);
+  act_form<T, MR, C, MODE>(p, lane, gw == 0, ra, xv);
 
   u32x4 fold = {0u, 0u, 0u, 0u};  // FLOOR: every loaded word is consumed here
   auto consume = [&](const Batch& B, int rb) {
@@ -993,12 +1020,15 @@ __global__ __launch_bounds__(kThreads) void w8a16_cyc_kernel(W8Params p) {
 #pragma unroll
     for (int c = 0; c < C; ++c) b[c] = sd::load16_stream(src + (koff[c] + z));
   };
+  // the activations' loads first, formed while the first two rows are in flight
+  RowActs<1, C, MODE> ra;
+  act_load<1, C, MODE>(p, lane, ra);
   Row buf[2];
   load_row(buf[0], 0, 0);
   load_row(buf[1], n > 1 ? 1 : 0, 0);
 
   float xv[1][C][16];
-  row_activations<T, 1, C, MODE>(p, lane, gw == 0, xv);
+  act_form<T, 1, C, MODE>(p, lane, gw == 0, ra, xv);
   // fp16: the activations as exact pairs, and 1152 times their sum (this lane's
   // columns): each weight byte enters the dot products as the exact fp16 value
   // 1152 + b, and the 1152 x sum is taken off once per row
