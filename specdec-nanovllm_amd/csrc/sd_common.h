@@ -424,6 +424,82 @@ __device__ __forceinline__ void add_rmsnorm_row_wave(const uint16_t* x, const ui
   }
 }
 
+// add_rmsnorm_row_wave for NR rows of H <= 1024 elements at once (H % 8 == 0):
+// rows r < nr exist, row r at x + r xs (res + r rs, out + r os, res_out +
+// r ros). Lane l holds the 8-element chunks l and 64 + l of each row, the
+// RMSNorm kernel's threads l and 64 + l (its waves 0 and 1; its waves 2 and 3
+// hold no chunk of such a row and add zeros). Every load goes out before the
+// first use, unconditionally (rows and columns clamped into the matrix, zeros
+// selected past H), and the row stays in registers between the sum and the
+// outputs; the wave sums are xor_sum_down's DPP steps. One round trip for all
+// NR rows, where add_rmsnorm_row_wave waits per chunk and reads the row twice.
+template <typename T, int NR>
+__device__ __forceinline__ void add_rmsnorm_rows_wave(const uint16_t* x, int64_t xs,
+                                                      const uint16_t* res, int64_t rs,
+                                                      const uint16_t* w, int H, float eps, int nr,
+                                                      uint16_t* out, int64_t os,
+                                                      uint16_t* res_out, int64_t ros) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  u32x4 a[NR][2], b[NR][2], wq[2];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int64_t rc = min(r, nr - 1);
+    const uint16_t* xr = x + rc * xs;
+    const uint16_t* br = res ? res + rc * rs : xr;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int e = min((v * 64 + lane) * 8, H - 8);
+      a[r][v] = load16(xr + e);
+      b[r][v] = load16(br + e);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 2; ++v) wq[v] = load16(w + min((v * 64 + lane) * 8, H - 8));
+  const bool has_res = res != nullptr;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    float val[2][8];
+    float tot = 0.f;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const bool ok = (v * 64 + lane) * 8 < H;
+      const uint32_t aw[4] = {a[r][v].x, a[r][v].y, a[r][v].z, a[r][v].w};
+      const uint32_t bw[4] = {b[r][v].x, b[r][v].y, b[r][v].z, b[r][v].w};
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float f = from_bits<T>(static_cast<uint16_t>(aw[i / 2] >> (16 * (i & 1))));
+        const float g = from_bits<T>(static_cast<uint16_t>(bw[i / 2] >> (16 * (i & 1))));
+        const float s = has_res ? f + g : f;
+        val[v][i] = ok ? s : 0.f;
+        ss += val[v][i] * val[v][i];
+      }
+      tot += xor_sum_down<32>(ss);  // the kernel's wave v
+    }
+    const float rn = rsqrtf(tot / static_cast<float>(H) + eps);
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int e0 = (v * 64 + lane) * 8;
+      const uint32_t ww[4] = {wq[v].x, wq[v].y, wq[v].z, wq[v].w};
+      uint32_t o[4], ro[4];
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const float w0 = from_bits<T>(static_cast<uint16_t>(ww[i / 2]));
+        const float w1 = from_bits<T>(static_cast<uint16_t>(ww[i / 2] >> 16));
+        const float n0 = static_cast<float>(round16<T>(val[v][i] * rn));
+        const float n1 = static_cast<float>(round16<T>(val[v][i + 1] * rn));
+        o[i / 2] = pack2<T>(n0 * w0, n1 * w1);
+        ro[i / 2] = pack2<T>(val[v][i], val[v][i + 1]);
+      }
+      if (e0 < H && r < nr) {
+        store16(out + r * os + e0, u32x4{o[0], o[1], o[2], o[3]});
+        if (res_out) store16(res_out + r * ros + e0, u32x4{ro[0], ro[1], ro[2], ro[3]});
+      }
+    }
+  }
+}
+
 // SiluAndMul on 8 elements: bf16(bf16(silu(g)) * u) per element (T = the
 // activation type), the eager module's roundings; g and u are 8 packed 16-bit
 // values each. Shared by the SiLU kernel and the W8A16 activation path that

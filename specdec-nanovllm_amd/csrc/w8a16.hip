@@ -543,10 +543,30 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
       // writes the residual sum. Every workgroup repeats this for its block.
       uint16_t* ro = p.nres && p.nres_out && blockIdx.x == 0 ? p.nres_out + m0 * p.nres_out_s : nullptr;
       const uint16_t* res = p.nres ? p.nres + m0 * p.nres_s : nullptr;
-      for (int r = wave; r < rows; r += NWV)
-        sd::add_rmsnorm_row_wave<T>(p.x + (m0 + r) * p.xs, res ? res + r * p.nres_s : nullptr, p.nw,
-                                    p.K, p.neps, reinterpret_cast<uint16_t*>(xsm + r * p.xpitch),
-                                    ro ? ro + r * p.nres_out_s : nullptr);
+      auto row_by_row = [&]() {
+        for (int r = wave; r < rows; r += NWV)
+          sd::add_rmsnorm_row_wave<T>(p.x + (m0 + r) * p.xs, res ? res + r * p.nres_s : nullptr, p.nw,
+                                      p.K, p.neps, reinterpret_cast<uint16_t*>(xsm + r * p.xpitch),
+                                      ro ? ro + r * p.nres_out_s : nullptr);
+      };
+      // up to 4 rows per wave and K <= 1024: each wave's rows in one call,
+      // every load of them in one round trip (a loop here would make the
+      // compiler wait for the weight prefetch at its head)
+      constexpr int NRW = (MT * 16 + NWV - 1) / NWV;
+      if constexpr (NRW <= 4) {
+        if (p.K <= 1024) {
+          const int r0 = wave * NRW;
+          if (r0 < rows)
+            sd::add_rmsnorm_rows_wave<T, NRW>(
+                p.x + (m0 + r0) * p.xs, p.xs, res ? res + r0 * p.nres_s : nullptr, p.nres_s, p.nw,
+                p.K, p.neps, min(NRW, rows - r0), reinterpret_cast<uint16_t*>(xsm + r0 * p.xpitch),
+                p.xpitch / 2, ro ? ro + r0 * p.nres_out_s : nullptr, p.nres_out_s);
+        } else {
+          row_by_row();
+        }
+      } else {
+        row_by_row();
+      }
     } else {
       for (int idx = tid; idx < rows * upr; idx += NTH) {
         const int r = idx / upr, c = idx - r * upr;

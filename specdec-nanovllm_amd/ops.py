@@ -377,8 +377,17 @@ def w8a16_silu_linear(gate_up: torch.Tensor, qweight: torch.Tensor, scale: torch
 
 
 # Rows up to which the add + RMSNorm runs inside the projection's launch (the
-# fused entry points accept more; past this the two launches measured faster).
-NORM_FUSED_MAX_ROWS = 4
+# fused entry points accept more; past this the two launches measured faster):
+# up to 16 rows of at most 1024 columns, where each wave of a workgroup
+# normalises up to 4 rows in one round trip, and up to 4 rows of wider ones,
+# where the waves take their rows one at a time.
+NORM_FUSED_MAX_ROWS = 16
+NORM_FUSED_MAX_ROWS_WIDE = 4
+
+
+def _norm_fused(M: int, K: int) -> bool:
+    limit = NORM_FUSED_MAX_ROWS if K <= 1024 else NORM_FUSED_MAX_ROWS_WIDE
+    return M <= limit and K % 8 == 0 and K <= 8192
 
 
 def w8a16_rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
@@ -393,11 +402,11 @@ def w8a16_rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     ``residual_out`` (sharing no byte with x, residual or the output; None:
     not written)
     receives bf16(x + residual), ``rmsnorm``'s second output. One launch for
-    up to 4 rows: at one or two rows every wave of the row-streaming GEMV
-    forms the norm of its columns; at three or four the tiled kernel's
-    workgroups normalise their rows while staging them (break-even near five
-    rows). More rows, or rows that do not fit the staging LDS, take the two
-    separate launches (same results)."""
+    up to 16 rows at K <= 1024 and up to 4 rows above: at one or two rows
+    every wave of the row-streaming GEMV forms the norm of its columns; from
+    three rows the tiled kernel's workgroups normalise their rows while
+    staging them. More rows, or rows that do not fit the staging LDS, take the
+    two separate launches (same results)."""
     assert qweight.dtype == torch.int8 and qweight.dim() == 2
     N, K = qweight.shape
     assert x.shape[-1] == K and norm_weight.shape == (K,)
@@ -430,7 +439,7 @@ def w8a16_rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     if M == 0:
         return y.view(shape)
     rc = _lib.SD_ERR_UNSUPPORTED
-    if M <= NORM_FUSED_MAX_ROWS and K % 8 == 0 and K <= 8192:
+    if _norm_fused(M, K):
         lib = _lib.load()
         with torch.cuda.device(dev):
             rc = lib.sd_w8a16_rmsnorm_linear(
@@ -505,10 +514,10 @@ def w8a16_gate_up_silu(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tens
         return y.view(shape)
     lib = _lib.load()
     xa, ra, roa, nwa = x2, r2, ro, nw
-    if nw is not None and M > NORM_FUSED_MAX_ROWS and K % 8 == 0 and K <= 8192:
-        # the staged norm pays at up to 4 rows (every workgroup normalises all of
-        # them): the RMSNorm launch (writing residual_out itself), then the
-        # paired projection on the normalised rows
+    if nw is not None and not _norm_fused(M, K) and K % 8 == 0 and K <= 8192:
+        # past the rows where the staged norm pays (every workgroup normalises
+        # all of them): the RMSNorm launch (writing residual_out itself), then
+        # the paired projection on the normalised rows
         xa = torch.empty_like(x2)
         rsum = ro if ro is not None or r2 is None else torch.empty_like(r2)
         with torch.cuda.device(dev):
