@@ -342,8 +342,7 @@ __device__ __forceinline__ void head_norm_rope(float x0, float x1, bool has_w, f
 #pragma clang fp contract(off)
   if (has_w) {
     float ss = x0 * x0 + x1 * x1;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    ss = xor_sum_down<32>(ss);  // the xor steps 32 .. 1
     const float r = rsqrtf(ss / 128.f + eps);
     x0 = static_cast<float>(round16<T>(static_cast<float>(round16<T>(x0 * r)) * w0));
     x1 = static_cast<float>(round16<T>(static_cast<float>(round16<T>(x1 * r)) * w1));

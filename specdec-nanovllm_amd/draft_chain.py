@@ -26,7 +26,7 @@ torch's argmax over a 151936-wide row clears its reduction semaphores with a
 memset, which a captured graph does not replay reliably), or this library's
 fused neighbour kernels with ``fused=True``:
 add + RMSNorm inside the projection that consumes it (qkv, gate_up, lm_head;
-at up to 4 rows, two launches beyond), q/k norm + RoPE + store_kvcache in one
+up to 16 rows at hidden 1024, two launches beyond), q/k norm + RoPE + store_kvcache in one
 launch on the qkv output (the attention reads q through strides), SiLU*mul in
 the gate_up projection's epilogue (one or two rows; the SiLU launch beyond),
 the sampler's argmax; the embedding lookup stays a torch index.
