@@ -526,6 +526,77 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
     c = wrap ? 0 : c + 1;
     g = wrap ? g + gstride : g;
   };
+  // XL staging: rows m0 .. m0 + rows of x (16-byte units), then the scale table
+  // (and bias) of the rows every wave of this workgroup owns; all waves take
+  // part. This thread's first SB units and first SC table entries load ahead of
+  // the weight prefetch, with no branch (indices clamped into range; entries
+  // past the end are loaded but not stored), so that waiting for them leaves
+  // the prefetch in flight. A load under a bounds branch or in a loop is waited
+  // for together with every load issued before it: the weight prefetch, then
+  // one round trip per unit (28 before the first MFMA at 56 rows of K = 1024).
+  // HOIST (whole rows per wave, no norm): SB activation units per thread and
+  // batch, what K = 1024 asks of a thread (at most 8, 4 with the up halves),
+  // and SC table entries per thread in the first batch. The K-split kernels
+  // (2 - 4 units per thread) measured slower with it at 56 rows (qkv 6.55 ->
+  // 6.91 us) and load one unit per thread and iteration; the norm's rows load
+  // after the prefetch anyway.
+  constexpr bool HOIST = XL && !NM && KW == 1;
+  constexpr int SBK = MT * 16 * 128 / NTH;
+  constexpr int SB = HOIST ? (SBK < 1 ? 1 : (SBK > (SL ? 4 : 8) ? (SL ? 4 : 8) : SBK)) : 1;
+  constexpr int SC = HOIST ? (NSUB * RG * 2 > NTH ? 2 : 1) : 0;
+  const int rows = XL ? min(MT * 16, p.M - m0) : 1;
+  const int upr = p.K / 8;  // 16-byte units per row
+  const int xtot = rows * upr;
+  const int per_sub = p.ngmax * RG;
+  const int stot = NSUB * per_sub * spr, btot = NSUB * per_sub;
+  auto unit_src = [&](int idx) {
+    idx = min(idx, xtot - 1);
+    const int r = idx / upr, c = idx - r * upr;
+    return p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8;
+  };
+  auto unit_dst = [&](int idx) {
+    const int r = idx / upr, c = idx - r * upr;
+    return xsm + r * p.xpitch + c * 16;
+  };
+  auto table_row = [&](int t) {  // weight row of table row t (clamped)
+    const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
+    const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
+    return min(wrow(g, r), nrows - 1);
+  };
+  auto scale_elem = [&](int idx) -> int64_t {  // scale element of table entry idx
+    idx = min(idx, max(stot, 1) - 1);
+    const int j = idx % spr, n = table_row(idx / spr);
+    return PER_GROUP ? static_cast<int64_t>(n) * spr + j : n;
+  };
+  // a scale as 16-bit halves at a uniform shift (fp32: two halves), the bias
+  // read from the scale when there is none: one load form, no branch
+  const int ssh = p.scale_dtype == SD_F32 ? 1 : 0;
+  const uint16_t* s16 = static_cast<const uint16_t*>(p.scale);
+  const uint16_t* bsrc = p.bias ? p.bias : s16;
+  const int64_t bmask = p.bias ? ~int64_t{0} : int64_t{0};
+  auto scale_val = [&](uint32_t h0, uint32_t h1) -> float {
+    if (ssh) return __uint_as_float(h0 | (h1 << 16));
+    const uint16_t h = static_cast<uint16_t>(h0);
+    return p.scale_dtype == SD_BF16 ? sd::from_bits<__bf16>(h) : sd::from_bits<_Float16>(h);
+  };
+  u32x4 xa[SB], xu[SL ? SB : 1];
+  uint32_t sh0[SC > 0 ? SC : 1], sh1[SC > 0 ? SC : 1];
+  uint16_t bv[SC > 0 ? SC : 1];
+  if constexpr (HOIST) {
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const uint16_t* src = unit_src(tid + j * NTH);
+      xa[j] = sd::load16(src);
+      if constexpr (SL) xu[j] = sd::load16(src + p.up);
+    }
+#pragma unroll
+    for (int j = 0; j < SC; ++j) {
+      const int64_t e = scale_elem(tid + j * NTH);
+      sh0[j] = s16[e << ssh];
+      sh1[j] = s16[(e << ssh) + ssh];
+      bv[j] = bsrc[static_cast<int64_t>(table_row(min(tid + j * NTH, max(btot, 1) - 1))) & bmask];
+    }
+  }
 #pragma unroll
   for (int d = 0; d < D - 1; ++d) {
     if (XL && nit == 0) break;
@@ -533,10 +604,6 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
     if (d + 1 < nit) advance(lgp, lcp);  // past the end: the last item again (dummy loads)
   }
   if constexpr (XL) {
-    // stage rows m0 .. m0 + rows of x (16-byte units) behind the first weight
-    // prefetch, so their latencies overlap; every wave of the workgroup takes part
-    const int rows = min(MT * 16, p.M - m0);
-    const int upr = p.K / 8;  // 16-byte units per row
     if constexpr (NM) {
       // one wave per row, the waves' rows at the same time (the RMSNorm
       // kernel's bits, sd::add_rmsnorm_row_wave); one workgroup per row block
@@ -568,30 +635,70 @@ __global__ __launch_bounds__(NWV * 64) void w8a16_kernel(W8Params p) {
         row_by_row();
       }
     } else {
-      for (int idx = tid; idx < rows * upr; idx += NTH) {
-        const int r = idx / upr, c = idx - r * upr;
-        const uint16_t* src = p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8;
-        if constexpr (SL)
-          sd::store16(xsm + r * p.xpitch + c * 16, sd::silu_mul8<T>(sd::load16(src), sd::load16(src + p.up)));
-        else
-          sd::store16(xsm + r * p.xpitch + c * 16, sd::load16(src));
+      // the first batch (loaded above), then SB units per thread at a time
+      auto put = [&](int b0) {
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+          const int idx = b0 + tid + j * NTH;
+          if (idx < xtot) {
+            if constexpr (SL) sd::store16(unit_dst(idx), sd::silu_mul8<T>(xa[j], xu[j]));
+            else sd::store16(unit_dst(idx), xa[j]);
+          }
+        }
+      };
+      if constexpr (HOIST) {
+        put(0);
+        for (int b0 = SB * NTH; b0 < xtot; b0 += SB * NTH) {
+#pragma unroll
+          for (int j = 0; j < SB; ++j) {
+            const uint16_t* src = unit_src(b0 + tid + j * NTH);
+            xa[j] = sd::load16(src);
+            if constexpr (SL) xu[j] = sd::load16(src + p.up);
+          }
+          put(b0);
+        }
+      } else {
+        for (int idx = tid; idx < xtot; idx += NTH) {
+          const int r = idx / upr, c = idx - r * upr;
+          const uint16_t* src = p.x + static_cast<int64_t>(m0 + r) * p.xs + c * 8;
+          if constexpr (SL)
+            sd::store16(xsm + r * p.xpitch + c * 16, sd::silu_mul8<T>(sd::load16(src), sd::load16(src + p.up)));
+          else
+            sd::store16(xsm + r * p.xpitch + c * 16, sd::load16(src));
+        }
       }
     }
-    // scales (and bias) of the rows every wave of this workgroup owns
-    const int per_sub = p.ngmax * RG;
-    for (int idx = tid; idx < NSUB * per_sub * spr; idx += NTH) {
-      const int j = idx % spr, t = idx / spr;
-      const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
-      const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
-      const int n = min(wrow(g, r), nrows - 1);
-      scl[idx] = load_scale(p.scale, p.scale_dtype,
-                            PER_GROUP ? static_cast<int64_t>(n) * spr + j : n);
-    }
-    if (p.bias) {
-      for (int t = tid; t < NSUB * per_sub; t += NTH) {
+    if constexpr (HOIST) {
+#pragma unroll
+      for (int j = 0; j < SC; ++j) {
+        const int idx = tid + j * NTH;
+        if (idx < stot) scl[idx] = scale_val(sh0[j], sh1[j]);
+        if (p.bias && idx < btot) bis[idx] = sd::from_bits<T>(bv[j]);
+      }
+      // table entries past the first batch (per-group scales, large tables)
+      for (int idx = SC * NTH + tid; idx < stot; idx += NTH) {
+        const int64_t e = scale_elem(idx);
+        scl[idx] = scale_val(s16[e << ssh], s16[(e << ssh) + ssh]);
+      }
+      if (p.bias) {
+        for (int t = SC * NTH + tid; t < btot; t += NTH)
+          bis[t] = sd::from_bits<T>(p.bias[table_row(t)]);
+      }
+    } else {
+      for (int idx = tid; idx < stot; idx += NTH) {
+        const int j = idx % spr, t = idx / spr;
         const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
         const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
-        bis[t] = sd::from_bits<T>(p.bias[min(wrow(g, r), nrows - 1)]);
+        const int n = min(wrow(g, r), nrows - 1);
+        scl[idx] = load_scale(p.scale, p.scale_dtype,
+                              PER_GROUP ? static_cast<int64_t>(n) * spr + j : n);
+      }
+      if (p.bias) {
+        for (int t = tid; t < btot; t += NTH) {
+          const int sb = t / per_sub, gi = (t - sb * per_sub) / RG, r = t % RG;
+          const int g = blockIdx.x * NSUB + sb + gi * gridDim.x * NSUB;
+          bis[t] = sd::from_bits<T>(p.bias[min(wrow(g, r), nrows - 1)]);
+        }
       }
     }
     __syncthreads();
