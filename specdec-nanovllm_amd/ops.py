@@ -481,7 +481,8 @@ def w8a16_gate_up_silu(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tens
     weights up to 32 MiB: a wave streams gate row i with up row I + i and
     forms the pair's SiLU once) and on the K-split path of narrow layers (a
     workgroup takes gate tile g and up tile g with the plain projection's K
-    split; with the norm, above 4 rows, the RMSNorm launch comes first);
+    split; with the norm, above 16 rows at K <= 1024 or 4 rows above, the
+    RMSNorm launch comes first);
     other shapes take the separate launches."""
     assert qweight.dtype == torch.int8 and qweight.dim() == 2
     N, K = qweight.shape
