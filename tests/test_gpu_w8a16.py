@@ -200,7 +200,13 @@ def test_silu_linear_is_silu_mul_then_linear(M, N, K, gs, act):
                                               (24, 33000, 1024, 0, torch.bfloat16, True),
                                               (48, 33000, 1024, 0, torch.bfloat16, True),
                                               (1, 151936, 1024, 0, torch.bfloat16, True),
-                                              (1, 16411, 2048, 0, torch.float16, False)])
+                                              (1, 16411, 2048, 0, torch.float16, False),
+                                              # staged 4 rows per wave: a short last wave,
+                                              # lanes past K, no residual
+                                              (13, 2048, 576, 0, torch.bfloat16, True),
+                                              (5, 4096, 1024, 0, torch.float16, False),
+                                              (16, 512, 64, 0, torch.bfloat16, True),
+                                              (11, 6144, 1024, 0, torch.bfloat16, True)])
 def test_rmsnorm_linear_is_rmsnorm_then_linear(M, N, K, gs, act, res):
     # add + RMSNorm formed while staging: bit-identical to rmsnorm then the
     # linear, residual_out identical to rmsnorm's (one row block per 16 or 32
@@ -311,7 +317,8 @@ def test_row_streaming_path(M, K, gs, act):
                                                 (16, 2048, 2048, torch.bfloat16, True, True),
                                                 (56, 6144, 1024, torch.float16, False, False),
                                                 (56, 6144, 1024, torch.bfloat16, True, True),
-                                                (5, 2064, 1024, torch.bfloat16, False, False)])
+                                                (5, 2064, 1024, torch.bfloat16, False, False),
+                                                (11, 6144, 1024, torch.bfloat16, True, False)])
 def test_gate_up_silu_is_linear_then_silu_mul(M, N, K, act, norm, res):
     """The gate_up projection with the SiLU epilogue (paired gate / up rows on
     the row-streaming path, paired gate / up tiles on the K-split path with the
