@@ -1514,21 +1514,29 @@ int launch_rows_c(const W8Params& p, hipStream_t st) {
       return SD_OK;
     }
   }
-  // about 4 weight rows per wave (2 output pairs with PAIR), at most two waves
-  // per SIMD (8 per CU)
+  // One weight row per wave (two output pairs with PAIR) up to two waves per
+  // SIMD (8 per CU), more rows per wave beyond; a batch holds the rows a wave
+  // owns (1, 2 or 4; 8 for long ranges). At one or two rows these launches are
+  // latency-bound, and more waves put more loads in flight at once: against 4
+  // rows per wave, the down projection (1024 x 3072) went 4.5 -> 3.2 us and
+  // o_proj (1024 x 2048) 3.7 -> 2.9 at M = 1 (1024 waves instead of 256).
   int64_t waves = static_cast<int64_t>(sd::device_cus()) * 8;
-  const int64_t want = PAIR ? (static_cast<int64_t>(p.N) + 1) / 2
-                            : (static_cast<int64_t>(p.N) + 3) / 4;
+  const int64_t want = PAIR ? (static_cast<int64_t>(p.N) + 1) / 2 : static_cast<int64_t>(p.N);
   if (want < waves) waves = want;
   const int blocks = static_cast<int>((waves + kWaves - 1) / kWaves);
   const int rpw = static_cast<int>((p.N + static_cast<int64_t>(blocks) * kWaves - 1) /
                                    (static_cast<int64_t>(blocks) * kWaves));
   if constexpr (PAIR) {
-    // 8 weight rows (4 pairs) per batch; 4 from three column chunks up, where
-    // two batches of 8 rows fill the register file
-    constexpr int RPAIR = C >= 3 ? 4 : 8;
-    hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, RPAIR, MODE, true, FLOOR>),
-                       dim3(blocks), dim3(kThreads), 0, st, p, rpw);
+    // 4 weight rows (2 pairs) per batch where a wave owns at most 2 pairs, or
+    // from three column chunks up (two batches of 8 rows would fill the
+    // register file); 8 rows (4 pairs) otherwise
+    if (C >= 3 || rpw <= 2) {
+      hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 4, MODE, true, FLOOR>), dim3(blocks),
+                         dim3(kThreads), 0, st, p, rpw);
+    } else {
+      hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, C >= 3 ? 4 : 8, MODE, true, FLOOR>),
+                         dim3(blocks), dim3(kThreads), 0, st, p, rpw);
+    }
     return SD_OK;
   }
   if constexpr (MR == 1 && C == 1) {
@@ -1538,8 +1546,16 @@ int launch_rows_c(const W8Params& p, hipStream_t st) {
       return SD_OK;
     }
   }
-  hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 4, MODE, false, FLOOR>), dim3(blocks),
-                     dim3(kThreads), 0, st, p, rpw);
+  if (rpw <= 1) {
+    hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 1, MODE, false, FLOOR>), dim3(blocks),
+                       dim3(kThreads), 0, st, p, rpw);
+  } else if (rpw <= 2) {
+    hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 2, MODE, false, FLOOR>), dim3(blocks),
+                       dim3(kThreads), 0, st, p, rpw);
+  } else {
+    hipLaunchKernelGGL((w8a16_rows_kernel<T, MR, C, 4, MODE, false, FLOOR>), dim3(blocks),
+                       dim3(kThreads), 0, st, p, rpw);
+  }
   return SD_OK;
 }
 
