@@ -1130,7 +1130,13 @@ Plan make_plan(int num_seqs, int max_qlen, int Hq, int Hkv, int num_splits) {
   // two waves per kv head, half the runs and partials: two row tiles (verify),
   // and small batches, whose pairs each collect a partial from many runs
   pl.KS = (pl.RT == 2 || num_seqs <= 4) && Hkv % 2 == 0 ? 2 : 1;
-  pl.NW = pl.TS == 2 ? 2 * pl.KS : (pl.KS == 2 ? 4 : (Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1)));
+  // Two key halves: one kv head per workgroup for a single sequence, two heads
+  // otherwise. One sequence of 2048 keys fills 33 runs, and two heads per
+  // workgroup then left half the CUs without work (C5 draft step B = 1 841 ->
+  // 832 us with one head; C2 decode B = 2 13.45 -> 13.75 us the other way).
+  pl.NW = pl.TS == 2 ? 2 * pl.KS
+                     : (pl.KS == 2 ? (num_seqs == 1 ? 2 : 4)
+                                   : (Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1)));
   int64_t runs;
   if (num_splits > 0) {
     runs = static_cast<int64_t>(num_splits) * num_seqs;
@@ -1187,7 +1193,8 @@ void launch_main(const AttnParams& p, const Plan& pl, hipStream_t st) {
     if (pl.KS == 2) launch_main<T, 1, STORE, 4, 2, FLOOR, 2>(p, st);
     else launch_main<T, 1, STORE, 2, 1, FLOOR, 2>(p, st);
   } else {
-    if (pl.KS == 2) launch_main<T, RT, STORE, 4, 2, FLOOR>(p, st);
+    if (pl.KS == 2 && pl.NW == 2) launch_main<T, RT, STORE, 2, 2, FLOOR>(p, st);
+    else if (pl.KS == 2) launch_main<T, RT, STORE, 4, 2, FLOOR>(p, st);
     else if (pl.NW == 4) launch_main<T, RT, STORE, 4, 1, FLOOR>(p, st);
     else if (pl.NW == 2) launch_main<T, RT, STORE, 2, 1, FLOOR>(p, st);
     else launch_main<T, RT, STORE, 1, 1, FLOOR>(p, st);
